@@ -1,0 +1,114 @@
+// Device helpers shared by the gfx950 kernels of the MoE path.
+//
+// Everything here is written for CDNA4 wave64: a "wave" is 64 lanes, reductions are xor
+// butterflies over 64 lanes.  Half-precision values travel as raw 16-bit patterns.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define DEV __device__ __forceinline__
+#define API extern "C" __attribute__((visibility("default")))
+
+namespace drm {
+
+constexpr int WAVE = 64;
+
+DEV float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
+DEV float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+DEV float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+DEV float f16f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN).
+DEV uint16_t to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Xor butterfly: after step o every lane holds a[l] + a[l ^ o]; IEEE addition commutes, so all
+// lanes end with the same bits and the result is one fixed summation tree.
+DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+DEV int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
+DEV int wave_id() { return (int)(threadIdx.x >> 6); }
+
+// Fast activations (tolerance paths only).
+DEV float silu(float x) { return x / (1.f + __expf(-x)); }
+DEV float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// int4 group scale/min pairs: one 32-bit word holds (scale, min) as two halves.
+struct ScaleF16 {
+  static DEV float2 pair(uint32_t w) { return make_float2(f16f(w & 0xffffu), f16f(w >> 16)); }
+};
+struct ScaleBF16 {
+  static DEV float2 pair(uint32_t w) { return make_float2(bf16_lo(w), bf16_hi(w)); }
+};
+
+// int8 scale of element k of row n for a K-wide int8 matrix.
+struct Q8G128F16 {  // reference layout: f16 scale per 128 inputs, s [N, K/128]
+  static DEV float scale(const uint16_t* s, size_t n, int k, int K) { return f16f(s[n * (K / 128) + (k >> 7)]); }
+  static constexpr bool per_row = false;
+};
+struct Q8RowBF16 {  // per-output-channel bf16 scale, s [N]
+  static DEV float scale(const uint16_t* s, size_t n, int, int) { return bf16f(s[n]); }
+  static constexpr bool per_row = true;
+};
+
+// Sum of 8 int4 nibbles of w times x[0..7] (x[i] pairs with nibble i = bits 4i..4i+3).
+// Masks the even and the odd nibbles into bytes so each value converts with one
+// v_cvt_f32_ubyteN.
+DEV float dot8_q4(uint32_t w, const float* x, float acc) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  acc = __builtin_fmaf((float)(lo & 0xff), x[0], acc);
+  acc = __builtin_fmaf((float)(hi & 0xff), x[1], acc);
+  acc = __builtin_fmaf((float)((lo >> 8) & 0xff), x[2], acc);
+  acc = __builtin_fmaf((float)((hi >> 8) & 0xff), x[3], acc);
+  acc = __builtin_fmaf((float)((lo >> 16) & 0xff), x[4], acc);
+  acc = __builtin_fmaf((float)((hi >> 16) & 0xff), x[5], acc);
+  acc = __builtin_fmaf((float)(lo >> 24), x[6], acc);
+  acc = __builtin_fmaf((float)(hi >> 24), x[7], acc);
+  return acc;
+}
+
+// Sum of 4 int8 values of w times x[0..3], computed as sum((b ^ 0x80) x) - 128 sum(x): the
+// caller subtracts 128 * sum(x) once per row slice.
+DEV float dot4_u8b(uint32_t w, const float* x, float acc) {
+  const uint32_t u = w ^ 0x80808080u;
+  acc = __builtin_fmaf((float)(u & 0xff), x[0], acc);
+  acc = __builtin_fmaf((float)((u >> 8) & 0xff), x[1], acc);
+  acc = __builtin_fmaf((float)((u >> 16) & 0xff), x[2], acc);
+  acc = __builtin_fmaf((float)(u >> 24), x[3], acc);
+  return acc;
+}
+
+// Plain 16-byte global load.
+DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+DEV uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
+
+// Touch [pf, pf + bytes) so the data sits in the memory-side cache (MALL) for the next
+// kernel.  Each block takes an equal share; the loaded words are folded into a register
+// that an empty asm statement consumes, so the loads stay live.
+DEV void warm_range(const char* pf, size_t bytes) {
+  if (!pf || !bytes) return;
+  const size_t nb = (size_t)gridDim.x * gridDim.y;
+  const size_t b = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const size_t per = ((bytes + nb - 1) / nb + 255) & ~(size_t)255;
+  const size_t b0 = b * per, b1 = b0 + per < bytes ? b0 + per : bytes;
+  uint32_t acc = 0;
+  for (size_t o = b0 + threadIdx.x * 64; o + 16 <= b1; o += (size_t)blockDim.x * 64) acc ^= ld16(pf + o).x;
+  asm volatile("" ::"v"(acc));
+}
+
+}  // namespace drm

@@ -1,0 +1,297 @@
+// Router: logits, softmax and top-k (reference: kernels/drama.cu:317-468, src/ffi.rs:41,55-59)
+// plus the bf16 GEMM dr_gemm that the prefill router uses (src/engine.rs:554).
+//
+// These kernels follow one canonical fp32 operation order, so the CPU oracle reproduces the
+// logits, the softmax probabilities and hence the selected experts bit for bit:
+//   RMSNorm  lane l accumulates x^2 over float4 indices l + 64 j with fmaf, 64-lane xor
+//            butterfly, t = ss * (1 / K) + eps, inv = canon_rsqrt(t), xn = (x * inv) * nw
+//   dot      lane l owns 8-element chunks l + 64 j, fmaf in element order, xor butterfly
+//   softmax  ex = exp(l - max) with the library's own exp (below), lane l sums experts
+//            l + 64 j in order, xor butterfly, p = ex / z (correctly rounded)
+//   top-k    k rounds of (p desc, index asc); total = sum of picked p in pick order;
+//            wts = p / total
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+using namespace drm;
+
+namespace {
+
+// exp: Cody-Waite reduction with k = rint(x log2 e), ln 2 split in a 16-bit head and a tail,
+// degree-8 Taylor polynomial of e^r in Horner form with fma, scaling by 2^k through the
+// exponent field.  Inputs below -86.5 give 0 and above 88 give +inf, so no subnormal result
+// is ever formed.  Accuracy: within 2 ulp of exp on the range that matters (x <= 0).
+DEV float canon_exp(float x) {
+  if (x != x) return x;
+  if (x < -86.5f) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  const float k = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(-k, 0.693145751953125f, x);
+  r = __builtin_fmaf(-k, 1.428606765330187e-06f, r);
+  float p = 2.48015873e-05f;
+  p = __builtin_fmaf(p, r, 1.98412698e-04f);
+  p = __builtin_fmaf(p, r, 1.38888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ki = (int)k;
+  return p * __uint_as_float((uint32_t)(ki + 127) << 23);
+}
+
+// 1 / sqrt(t) for t > 0 from plain multiplies and subtractions only, so every step rounds
+// the same way on any IEEE machine: seed from the exponent/mantissa bit pattern
+// (0x5f3759df - bits / 2), then three Newton steps y = y * (1.5 - (0.5 t) * (y * y)).
+// Relative error <= 2e-7.  Nothing here may be contracted into an fma (this file is compiled
+// with contraction off and uses no header math helpers).
+DEV float canon_rsqrt(float t) {
+  float y = __uint_as_float(0x5f3759dfu - (__float_as_uint(t) >> 1));
+  const float h = 0.5f * t;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float yy = y * y;
+    const float hyy = h * yy;
+    const float c = 1.5f - hyy;
+    y = y * c;
+  }
+  return y;
+}
+
+// Canonical 1 / sqrt(mean(x^2) + eps) of a K-float vector; every lane of the wave gets it.
+template <int K>
+DEV float canon_rms_inv(const float* __restrict__ x, float eps) {
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = lane_id(); c < K / 4; c += WAVE) {
+    const float4 v = x4[c];
+    ss = __builtin_fmaf(v.x, v.x, ss);
+    ss = __builtin_fmaf(v.y, v.y, ss);
+    ss = __builtin_fmaf(v.z, v.z, ss);
+    ss = __builtin_fmaf(v.w, v.w, ss);
+  }
+  ss = wave_sum(ss);
+  const float t = ss * (1.0f / (float)K) + eps;
+  return canon_rsqrt(t);
+}
+
+// Softmax + top-k of one row of logits by one wave; lane k < topk receives pick k.
+DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* my_idx, float* my_w) {
+  const int lane = lane_id();
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + WAVE * j;
+    v[j] = e < E ? l[e] : -__builtin_inff();
+  }
+  const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+  float ex[4], z = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + WAVE * j;
+    ex[j] = e < E ? canon_exp(v[j] - m) : 0.f;
+    z = z + ex[j];
+  }
+  z = wave_sum(z);
+  float p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = (lane + WAVE * j) < E ? ex[j] / z : -1.f;
+  float total = 0.f, w = 0.f;
+  int id = 0;
+  for (int k = 0; k < topk; ++k) {
+    float bv = -2.f;
+    int bi = 1 << 30;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (p[j] > bv) bv = p[j], bi = lane + WAVE * j;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, WAVE);
+      const int oi = __shfl_xor(bi, o, WAVE);
+      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + WAVE * j == bi) p[j] = -1.f;
+    total = total + bv;
+    if (lane == k) w = bv, id = bi;
+  }
+  *my_idx = id;
+  *my_w = w / total;
+}
+
+// Decode router: wave w of block b computes logit row 4 b + w of the E + 1 rows; the last
+// block to finish (atomic counter) runs softmax/top-k with its first wave and resets the
+// counter.
+template <int K>
+__global__ void __launch_bounds__(256)
+    k_router_topk(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ nw,
+                  float eps, float* __restrict__ logits, int E, int topk, int* __restrict__ idx,
+                  float* __restrict__ wts, float* __restrict__ sgate, uint32_t* __restrict__ counter) {
+  __shared__ int s_last;
+  const int lane = lane_id(), wave = wave_id();
+  const int row = blockIdx.x * 4 + wave;
+  if (row <= E) {
+    constexpr int NCH = K / 8 / WAVE;
+    uint4 w[NCH];
+    const uint16_t* wr = W + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) w[j] = ld16(wr + (size_t)(lane + WAVE * j) * 8);
+    const float inv = nw ? canon_rms_inv<K>(x, eps) : 1.f;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* n4 = reinterpret_cast<const float4*>(nw);
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + WAVE * j;
+      float4 a = x4[2 * c], b = x4[2 * c + 1];
+      if (nw) {
+        const float4 na = n4[2 * c], nb = n4[2 * c + 1];
+        a = make_float4((a.x * inv) * na.x, (a.y * inv) * na.y, (a.z * inv) * na.z, (a.w * inv) * na.w);
+        b = make_float4((b.x * inv) * nb.x, (b.y * inv) * nb.y, (b.z * inv) * nb.z, (b.w * inv) * nb.w);
+      }
+      acc = __builtin_fmaf(bf16_lo(w[j].x), a.x, acc);
+      acc = __builtin_fmaf(bf16_hi(w[j].x), a.y, acc);
+      acc = __builtin_fmaf(bf16_lo(w[j].y), a.z, acc);
+      acc = __builtin_fmaf(bf16_hi(w[j].y), a.w, acc);
+      acc = __builtin_fmaf(bf16_lo(w[j].z), b.x, acc);
+      acc = __builtin_fmaf(bf16_hi(w[j].z), b.y, acc);
+      acc = __builtin_fmaf(bf16_lo(w[j].w), b.z, acc);
+      acc = __builtin_fmaf(bf16_hi(w[j].w), b.w, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[row] = acc;
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last || wave != 0) return;
+  __threadfence();
+  int my_idx;
+  float my_w;
+  canon_softmax_topk(logits, E, topk, &my_idx, &my_w);
+  if (lane < topk) idx[lane] = my_idx, wts[lane] = my_w;
+  if (lane == 0) {
+    sgate[0] = logits[E];
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ void __launch_bounds__(64)
+    k_moe_topk(const float* __restrict__ logits, int E, int topk, int stride, int* __restrict__ idx,
+               float* __restrict__ wts, float* __restrict__ sgate) {
+  const int r = blockIdx.x, lane = lane_id();
+  const float* l = logits + (size_t)r * stride;
+  int my_idx;
+  float my_w;
+  canon_softmax_topk(l, E, topk, &my_idx, &my_w);
+  if (lane < topk) idx[(size_t)r * topk + lane] = my_idx, wts[(size_t)r * topk + lane] = my_w;
+  if (lane == 0) sgate[r] = l[E];
+}
+
+// Canonical bf16 GEMM C = A . W^T (+ beta C).  Block = 4 waves; wave w holds MPW rows of A
+// (its lane chunks, as fp32) in registers and walks BN rows of W.  NCH = chunks per lane.
+constexpr int GM_MPW = 4, GM_BN = 32;
+
+template <int NCH>
+__global__ void __launch_bounds__(256)
+    k_gemm_canon(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W, float* __restrict__ C, int M,
+                 int N, int K, float beta) {
+  const int lane = lane_id(), wave = wave_id();
+  const int m0 = (blockIdx.x * 4 + wave) * GM_MPW;
+  const int n0 = blockIdx.y * GM_BN;
+  const int KC = K / 8;
+  float a[GM_MPW][NCH * 8];
+#pragma unroll
+  for (int r = 0; r < GM_MPW; ++r) {
+    const int m = m0 + r < M ? m0 + r : M - 1;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + WAVE * j;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (c < KC) v = ld16(A + (size_t)m * K + (size_t)c * 8);
+      a[r][8 * j + 0] = bf16_lo(v.x), a[r][8 * j + 1] = bf16_hi(v.x);
+      a[r][8 * j + 2] = bf16_lo(v.y), a[r][8 * j + 3] = bf16_hi(v.y);
+      a[r][8 * j + 4] = bf16_lo(v.z), a[r][8 * j + 5] = bf16_hi(v.z);
+      a[r][8 * j + 6] = bf16_lo(v.w), a[r][8 * j + 7] = bf16_hi(v.w);
+    }
+  }
+  for (int nn = 0; nn < GM_BN; ++nn) {
+    const int n = n0 + nn;
+    if (n >= N) break;
+    uint4 w[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + WAVE * j;
+      w[j] = c < KC ? ld16(W + (size_t)n * K + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < GM_MPW; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        if (lane + WAVE * j < KC) {
+          const float* av = &a[r][8 * j];
+          acc = __builtin_fmaf(bf16_lo(w[j].x), av[0], acc);
+          acc = __builtin_fmaf(bf16_hi(w[j].x), av[1], acc);
+          acc = __builtin_fmaf(bf16_lo(w[j].y), av[2], acc);
+          acc = __builtin_fmaf(bf16_hi(w[j].y), av[3], acc);
+          acc = __builtin_fmaf(bf16_lo(w[j].z), av[4], acc);
+          acc = __builtin_fmaf(bf16_hi(w[j].z), av[5], acc);
+          acc = __builtin_fmaf(bf16_lo(w[j].w), av[6], acc);
+          acc = __builtin_fmaf(bf16_hi(w[j].w), av[7], acc);
+        }
+      }
+      acc = wave_sum(acc);
+      const int m = m0 + r;
+      if (lane == 0 && m < M) {
+        float* c = C + (size_t)m * N + n;
+        *c = beta == 0.f ? acc : acc + beta * *c;
+      }
+    }
+  }
+}
+
+template <int NCH>
+void launch_gemm(const uint16_t* A, const uint16_t* W, float* C, int M, int N, int K, float beta, hipStream_t st) {
+  const dim3 g((M + 4 * GM_MPW - 1) / (4 * GM_MPW), (N + GM_BN - 1) / GM_BN);
+  hipLaunchKernelGGL(k_gemm_canon<NCH>, g, dim3(256), 0, st, A, W, C, M, N, K, beta);
+}
+
+}  // namespace
+
+hipStream_t gemm_handle_stream(void* h);
+
+API int dr_router_topk(const uint16_t* W, const float* x, const float* nw, float eps, float* logits, int E, int topk,
+                       int K, int* idx, float* wts, float* sgate, uint32_t* counter, const char*, const char*,
+                       const char*, const char*, size_t, size_t, size_t, size_t, hipStream_t st) {
+  if (K != 2048 || E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E) return -1;
+  hipLaunchKernelGGL(k_router_topk<2048>, dim3((E + 1 + 3) / 4), dim3(256), 0, st, W, x, nw, eps, logits, E, topk,
+                     idx, wts, sgate, counter);
+  return 0;
+}
+
+API int dr_moe_topk(const float* logits, int rows, int E, int topk, int stride, int* idx, float* wts, float* sgate,
+                    hipStream_t st) {
+  if (E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E || stride < E + 1) return -1;
+  if (rows <= 0) return 0;
+  hipLaunchKernelGGL(k_moe_topk, dim3(rows), dim3(64), 0, st, logits, E, topk, stride, idx, wts, sgate);
+  return 0;
+}
+
+API int dr_gemm(void* h, const uint16_t* A, const uint16_t* W, float* C, int M, int N, int K, float beta) {
+  if (K % 8 != 0 || K <= 0 || M < 0 || N < 0) return -1;
+  if (M == 0 || N == 0) return 0;
+  hipStream_t st = gemm_handle_stream(h);
+  const int kc = K / 8;
+  if (kc <= 64) launch_gemm<1>(A, W, C, M, N, K, beta, st);
+  else if (kc <= 128) launch_gemm<2>(A, W, C, M, N, K, beta, st);
+  else if (kc <= 256) launch_gemm<4>(A, W, C, M, N, K, beta, st);
+  else if (kc <= 512) launch_gemm<8>(A, W, C, M, N, K, beta, st);
+  else return -1;
+  return 0;
+}

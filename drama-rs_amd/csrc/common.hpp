@@ -27,18 +27,81 @@ DEV uint16_t to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-// Xor butterfly: after step o every lane holds a[l] + a[l ^ o]; IEEE addition commutes, so all
-// lanes end with the same bits and the result is one fixed summation tree.
+// Cross-lane exchange for the ascending xor butterfly o = 1, 2, 4, 8, 16, 32.
+//   o = 1, 2: DPP quad_perm, the exact xor partner;
+//   o = 4, 8: DPP row_half_mirror / row_mirror (lane 7 - i, 15 - i); after the lower steps every
+//             quad (octet) holds one value, so the mirrored lane carries the xor partner's bits;
+//   o = 16, 32: v_permlane16_swap / v_permlane32_swap of the value with itself, which hands
+//             every lane both halves (lo, hi) of the pair.
+// Every combine is a commutative op on the two halves, so all 64 lanes end with identical bits
+// and the result is one fixed tree: step o combines a[l] and a[l ^ o].  All lanes must be active.
+template <int O>
+DEV void xchg(float v, float& lo, float& hi) {
+  if constexpr (O == 1 || O == 2 || O == 4 || O == 8) {
+    constexpr int ctrl = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x141 : 0x140;
+    lo = v;
+    hi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+  } else if constexpr (O == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
+  } else {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
+  }
+}
+
+template <int O>
+DEV float xsum_step(float v) {
+  float a, b;
+  xchg<O>(v, a, b);
+  return a + b;
+}
+
+// Sum over the wave with the ascending xor tree (see xchg); every lane gets the same bits.
 DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+  v = xsum_step<1>(v);
+  v = xsum_step<2>(v);
+  v = xsum_step<4>(v);
+  v = xsum_step<8>(v);
+  v = xsum_step<16>(v);
+  return xsum_step<32>(v);
+}
+
+template <int O>
+DEV float xmax_step(float v) {
+  float a, b;
+  xchg<O>(v, a, b);
+  return fmaxf(a, b);
 }
 
 DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-  return v;
+  v = xmax_step<1>(v);
+  v = xmax_step<2>(v);
+  v = xmax_step<4>(v);
+  v = xmax_step<8>(v);
+  v = xmax_step<16>(v);
+  return xmax_step<32>(v);
+}
+
+// (value, index) pair of the wave maximum: larger value first, lower index on ties.
+template <int O>
+DEV void xarg_step(float& v, int& i) {
+  float va, vb, ia, ib;
+  xchg<O>(v, va, vb);
+  xchg<O>(__int_as_float(i), ia, ib);
+  const int a = __float_as_int(ia), b = __float_as_int(ib);
+  const bool take_b = vb > va || (vb == va && b < a);
+  v = take_b ? vb : va;
+  i = take_b ? b : a;
+}
+
+DEV void wave_argmax(float& v, int& i) {
+  xarg_step<1>(v, i);
+  xarg_step<2>(v, i);
+  xarg_step<4>(v, i);
+  xarg_step<8>(v, i);
+  xarg_step<16>(v, i);
+  xarg_step<32>(v, i);
 }
 
 DEV int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }

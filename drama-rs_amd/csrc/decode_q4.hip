@@ -31,25 +31,23 @@ DEV void stage_xn(const float* __restrict__ x, const float* __restrict__ nw, flo
   __shared__ float red[4];
   const float4* x4 = reinterpret_cast<const float4*>(x);
   constexpr int PER = H / 4 / 256;
-  float4 v[PER];
+  float4 v[PER], w[PER];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    v[i] = x4[threadIdx.x + 256 * i];
-    ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-  }
-  float inv = 1.f;
+  for (int i = 0; i < PER; ++i) v[i] = x4[threadIdx.x + 256 * i];
   if (nw) {
+    const float4* n4 = reinterpret_cast<const float4*>(nw);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) w[i] = n4[threadIdx.x + 256 * i];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     ss = wave_sum(ss);
     if (lane_id() == 0) red[wave_id()] = ss;
     __syncthreads();
-    inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
-    const float4* n4 = reinterpret_cast<const float4*>(nw);
+    const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float4 w = n4[threadIdx.x + 256 * i];
-      v[i] = make_float4(v[i].x * inv * w.x, v[i].y * inv * w.y, v[i].z * inv * w.z, v[i].w * inv * w.w);
-    }
+    for (int i = 0; i < PER; ++i)
+      v[i] = make_float4(v[i].x * inv * w[i].x, v[i].y * inv * w[i].y, v[i].z * inv * w[i].z, v[i].w * inv * w[i].w);
   }
 #pragma unroll
   for (int i = 0; i < PER; ++i) xs[slot(threadIdx.x + 256 * i)] = v[i];

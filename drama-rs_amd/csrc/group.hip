@@ -1,0 +1,224 @@
+// Prefill grouping of (row, k) pairs by expert (reference: kernels/drama.cu:744-797,
+// src/engine.rs:564-575) and the weighted combine.
+//
+// dr_moe_group is one workgroup of 16 waves: a stable counting sort in three phases.
+//   1. wave w takes chunks of 128 pairs; for each 64-pair half it finds, with 8 ballots over
+//      the expert-id bits, the lanes that share its expert: the rank within the chunk is the
+//      count of lower such lanes, the chunk count goes to a [chunk][expert] table in LDS;
+//   2. thread e scans its expert's column over the chunks (exclusive), giving each chunk's
+//      base and the expert's total; a block scan over experts gives the offsets;
+//   3. slot = offsets[e] + base[chunk][e] + rank.
+// The order within an expert is ascending pair index (the reference's atomics give an
+// unspecified order; this is one of its possible outcomes, and the CPU oracle's).
+#include "common.hpp"
+
+using namespace drm;
+
+namespace {
+
+constexpr int GR_THREADS = 1024, GR_WAVES = GR_THREADS / 64, GR_CHUNK = 128, GR_MAXN = 8192;
+constexpr int GR_MAXCH = GR_MAXN / GR_CHUNK;  // 64 chunks
+
+// mask of lanes whose 8-bit key equals this lane's
+DEV uint64_t match8(uint32_t key, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (key >> b) & 1u;
+    const uint64_t bal = __ballot(bit && valid);
+    m &= bit ? bal : ~bal;
+  }
+  return m;
+}
+
+// mode 0: compute counts/offsets and slots; mode 1: offsets given (dr_moe_permute), also fill
+__global__ void __launch_bounds__(GR_THREADS)
+    k_group(const int* __restrict__ idx, int n, int E, int* __restrict__ counts, int* __restrict__ offsets,
+            int* __restrict__ slot_of, int mode, int* __restrict__ fill) {
+  __shared__ uint16_t tab[GR_MAXCH][256];  // per-chunk count, then per-chunk base
+  __shared__ uint8_t rank[GR_MAXN];
+  __shared__ int s_off[256];
+  __shared__ int s_wsum[GR_WAVES];
+  const int lane = lane_id(), wave = wave_id();
+  const int nch = (n + GR_CHUNK - 1) / GR_CHUNK;
+  for (int i = threadIdx.x; i < GR_MAXCH * 256; i += GR_THREADS) (&tab[0][0])[i] = 0;
+  __syncthreads();
+  for (int c = wave; c < nch; c += GR_WAVES) {
+    for (int h = 0; h < 2; ++h) {
+      const int i = c * GR_CHUNK + h * 64 + lane;
+      const bool valid = i < n;
+      const uint32_t key = valid ? (uint32_t)idx[i] & 255u : 0u;  // ids must be < E <= 256
+      const uint64_t m = match8(key, valid);
+      const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+      const int r = __popcll(m & lower);
+      // earlier half's count of the same key: read from the table (written below by the leader)
+      __builtin_amdgcn_wave_barrier();
+      const int prev = valid ? (int)tab[c][key] : 0;
+      __builtin_amdgcn_wave_barrier();
+      if (valid) rank[i] = (uint8_t)(prev + r);
+      const bool leader = valid && r == 0;
+      if (leader) tab[c][key] = (uint16_t)(prev + __popcll(m));
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __syncthreads();
+  // phase 2: per-expert exclusive scan over chunks; totals
+  int total = 0;
+  if (threadIdx.x < 256) {
+    const int e = threadIdx.x;
+    for (int c = 0; c < nch; ++c) {
+      const int v = tab[c][e];
+      tab[c][e] = (uint16_t)total;
+      total += v;
+    }
+  }
+  // block-wide exclusive scan of totals over experts 0..255 (waves 0..3)
+  if (threadIdx.x < 256) {
+    int v = total;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, 64);
+      if (lane >= o) v += t;
+    }
+    if (lane == 63) s_wsum[wave] = v;
+    s_off[threadIdx.x] = v - total;  // exclusive within the wave
+  }
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += s_wsum[w];
+    const int e = threadIdx.x;
+    const int off = mode == 0 ? s_off[e] + base : offsets[e];
+    s_off[e] = off;
+    if (e < E) {
+      if (mode == 0) counts[e] = total, offsets[e] = off;
+      else fill[e] = total;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += GR_THREADS) {
+    const int e = idx[i] & 255, c = i / GR_CHUNK;
+    slot_of[i] = s_off[e] + (int)tab[c][e] + (int)rank[i];
+  }
+}
+
+// xp[slot_of[i]] = x[i / topk]: 16 bytes per thread, one pair per 256-thread block.
+__global__ void __launch_bounds__(256)
+    k_gather_rows(const int* __restrict__ slot_of, int topk, const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                  int H) {
+  const int i = blockIdx.x;
+  const int slot = slot_of[i];
+  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)(i / topk) * H);
+  uint4* dst = reinterpret_cast<uint4*>(xp + (size_t)slot * H);
+  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) dst[c] = src[c];
+}
+
+__global__ void k_count(const int* __restrict__ idx, int n, int* __restrict__ counts) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) atomicAdd(counts + idx[i], 1);
+}
+
+// x[r, c] += sigmoid(sgate[r]) * shared[r, c] + sum_k wts[r, k] * y[slot_of[r, k], c], k ascending.
+__global__ void __launch_bounds__(256)
+    k_combine(float* __restrict__ x, const float* __restrict__ y, const int* __restrict__ slot_of,
+              const float* __restrict__ wts, const float* __restrict__ sgate, const float* __restrict__ shared,
+              int topk, int H) {
+  const int r = blockIdx.x;
+  const float sg = sigmoid(sgate[r]);
+  for (int c = threadIdx.x * 4; c < H; c += blockDim.x * 4) {
+    const float4 sh = *reinterpret_cast<const float4*>(shared + (size_t)r * H + c);
+    float4 acc = make_float4(sg * sh.x, sg * sh.y, sg * sh.z, sg * sh.w);
+    for (int k = 0; k < topk; ++k) {
+      const float w = wts[r * topk + k];
+      const float4 v = *reinterpret_cast<const float4*>(y + (size_t)slot_of[r * topk + k] * H + c);
+      acc.x += w * v.x, acc.y += w * v.y, acc.z += w * v.z, acc.w += w * v.w;
+    }
+    float4* xo = reinterpret_cast<float4*>(x + (size_t)r * H + c);
+    float4 o = *xo;
+    o.x += acc.x, o.y += acc.y, o.z += acc.z, o.w += acc.w;
+    *xo = o;
+  }
+}
+
+__global__ void k_dequant_q8(const int8_t* __restrict__ W, const uint16_t* __restrict__ S, uint16_t* __restrict__ out,
+                             size_t n, int K) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const size_t row = i / K, col = i % K;
+  out[i] = to_bf16((float)W[i] * f16f(S[row * (K / 128) + col / 128]));
+}
+
+__global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = to_bf16(x[i]);
+}
+
+__global__ void k_swiglu_rows(const float* __restrict__ h, uint16_t* __restrict__ y, int rows, int I) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * I) return;
+  const size_t r = i / I, j = i % I;
+  y[i] = to_bf16(silu(h[r * 2 * I + j]) * h[r * 2 * I + I + j]);
+}
+
+}  // namespace
+
+API int dr_moe_group(const int* idx, int n, int E, int* counts, int* offsets, int* slot_of, hipStream_t st) {
+  if (n < 0 || n > GR_MAXN || E < 1 || E > 256) return -1;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, E, counts, offsets, slot_of, 0, nullptr);
+  return 0;
+}
+
+API int dr_moe_gather_rows(const int* slot_of, int rows, int topk, const uint16_t* x, uint16_t* xp, int H,
+                           hipStream_t st) {
+  if (H % 8 != 0 || rows < 0 || topk < 1) return -1;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(k_gather_rows, dim3(rows * topk), dim3(256), 0, st, slot_of, topk, x, xp, H);
+  return 0;
+}
+
+API int dr_moe_count(const int* idx, int n, int* counts, hipStream_t st) {
+  if (n < 0) return -1;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_count, dim3((n + 255) / 256), dim3(256), 0, st, idx, n, counts);
+  return 0;
+}
+
+API int dr_moe_permute(const int* idx, int rows, int topk, const int* offsets, int* fill, int* slot_of,
+                       const uint16_t* x, uint16_t* xp, int H, hipStream_t st) {
+  const int n = rows * topk;
+  if (n < 0 || n > GR_MAXN || H % 8 != 0 || topk < 1) return -1;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, 256, nullptr, const_cast<int*>(offsets),
+                     slot_of, 1, fill);
+  hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(256), 0, st, slot_of, topk, x, xp, H);
+  return 0;
+}
+
+API int dr_moe_combine(float* x, const float* y, const int* slot_of, const float* wts, const float* sgate,
+                       const float* shared, int rows, int topk, int H, hipStream_t st) {
+  if (topk < 1 || topk > 32 || H % 4 != 0) return -1;
+  if (rows <= 0) return 0;
+  hipLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, x, y, slot_of, wts, sgate, shared, topk, H);
+  return 0;
+}
+
+API int dr_dequant_q8(const int8_t* W, const uint16_t* S, uint16_t* out, int N, int K, hipStream_t st) {
+  if (K % 128 != 0) return -1;
+  const size_t n = (size_t)N * K;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_dequant_q8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, W, S, out, n, K);
+  return 0;
+}
+
+API int dr_f32_to_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_f32_to_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+  return 0;
+}
+
+API int dr_swiglu_rows(const float* h, uint16_t* y, int rows, int I, hipStream_t st) {
+  const size_t n = (size_t)rows * I;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_swiglu_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, h, y, rows, I);
+  return 0;
+}

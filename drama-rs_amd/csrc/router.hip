@@ -107,12 +107,7 @@ DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* m
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (p[j] > bv) bv = p[j], bi = lane + WAVE * j;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, WAVE);
-      const int oi = __shfl_xor(bi, o, WAVE);
-      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
-    }
+    wave_argmax(bv, bi);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (lane + WAVE * j == bi) p[j] = -1.f;
@@ -123,35 +118,65 @@ DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* m
   *my_w = w / total;
 }
 
-// Decode router: wave w of block b computes logit row 4 b + w of the E + 1 rows; the last
-// block to finish (atomic counter) runs softmax/top-k with its first wave and resets the
-// counter.
+constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
+
+// Decode router: wave w of block b computes logit row RT_WPB b + w of the E + 1 rows.  All
+// loads of a wave (its weight row, x for the norm, x and nw for its dot lanes) are issued
+// before any arithmetic.  Logits are published with cache-bypassing (sc1) stores; after its
+// stores have completed (s_waitcnt) each block counts itself in with one relaxed atomic, and
+// the last block reads the logits back with sc1 loads and runs softmax/top-k with its first
+// wave.  No cache-maintenance fence is needed: every cross-block value bypasses the
+// non-coherent caches.  The last block resets the counter for the next call.
 template <int K>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(RT_WPB * 64)
     k_router_topk(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ nw,
                   float eps, float* __restrict__ logits, int E, int topk, int* __restrict__ idx,
                   float* __restrict__ wts, float* __restrict__ sgate, uint32_t* __restrict__ counter) {
   __shared__ int s_last;
   const int lane = lane_id(), wave = wave_id();
-  const int row = blockIdx.x * 4 + wave;
+  const int row = blockIdx.x * RT_WPB + wave;
   if (row <= E) {
-    constexpr int NCH = K / 8 / WAVE;
+    constexpr int NCH = K / 8 / WAVE, NRM = K / 4 / WAVE;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* n4 = reinterpret_cast<const float4*>(nw);
     uint4 w[NCH];
+    float4 xa[NCH], xb[NCH], na[NCH], nb[NCH], xr[NRM];
     const uint16_t* wr = W + (size_t)row * K;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) w[j] = ld16(wr + (size_t)(lane + WAVE * j) * 8);
-    const float inv = nw ? canon_rms_inv<K>(x, eps) : 1.f;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const float4* n4 = reinterpret_cast<const float4*>(nw);
-    float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + WAVE * j;
-      float4 a = x4[2 * c], b = x4[2 * c + 1];
+      xa[j] = x4[2 * c], xb[j] = x4[2 * c + 1];
+    }
+    float inv = 1.f;
+    if (nw) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + WAVE * j;
+        na[j] = n4[2 * c], nb[j] = n4[2 * c + 1];
+      }
+#pragma unroll
+      for (int j = 0; j < NRM; ++j) xr[j] = x4[lane + WAVE * j];
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NRM; ++j) {
+        ss = __builtin_fmaf(xr[j].x, xr[j].x, ss);
+        ss = __builtin_fmaf(xr[j].y, xr[j].y, ss);
+        ss = __builtin_fmaf(xr[j].z, xr[j].z, ss);
+        ss = __builtin_fmaf(xr[j].w, xr[j].w, ss);
+      }
+      ss = wave_sum(ss);
+      const float t = ss * (1.0f / (float)K) + eps;
+      inv = canon_rsqrt(t);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      float4 a = xa[j], b = xb[j];
       if (nw) {
-        const float4 na = n4[2 * c], nb = n4[2 * c + 1];
-        a = make_float4((a.x * inv) * na.x, (a.y * inv) * na.y, (a.z * inv) * na.z, (a.w * inv) * na.w);
-        b = make_float4((b.x * inv) * nb.x, (b.y * inv) * nb.y, (b.z * inv) * nb.z, (b.w * inv) * nb.w);
+        a = make_float4((a.x * inv) * na[j].x, (a.y * inv) * na[j].y, (a.z * inv) * na[j].z, (a.w * inv) * na[j].w);
+        b = make_float4((b.x * inv) * nb[j].x, (b.y * inv) * nb[j].y, (b.z * inv) * nb[j].z, (b.w * inv) * nb[j].w);
       }
       acc = __builtin_fmaf(bf16_lo(w[j].x), a.x, acc);
       acc = __builtin_fmaf(bf16_hi(w[j].x), a.y, acc);
@@ -163,20 +188,25 @@ __global__ void __launch_bounds__(256)
       acc = __builtin_fmaf(bf16_hi(w[j].w), b.w, acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) logits[row] = acc;
+    if (lane == 0) __hip_atomic_store(logits + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
   if (!s_last || wave != 0) return;
-  __threadfence();
+  // stage the logits (sc1 loads) into registers of wave 0, then the canonical softmax/top-k
+  __shared__ float lg[257];
+  for (int e = lane; e <= E; e += WAVE) lg[e] = __hip_atomic_load(logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
   int my_idx;
   float my_w;
-  canon_softmax_topk(logits, E, topk, &my_idx, &my_w);
+  canon_softmax_topk(lg, E, topk, &my_idx, &my_w);
   if (lane < topk) idx[lane] = my_idx, wts[lane] = my_w;
   if (lane == 0) {
-    sgate[0] = logits[E];
+    sgate[0] = lg[E];
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -270,7 +300,7 @@ API int dr_router_topk(const uint16_t* W, const float* x, const float* nw, float
                        int K, int* idx, float* wts, float* sgate, uint32_t* counter, const char*, const char*,
                        const char*, const char*, size_t, size_t, size_t, size_t, hipStream_t st) {
   if (K != 2048 || E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E) return -1;
-  hipLaunchKernelGGL(k_router_topk<2048>, dim3((E + 1 + 3) / 4), dim3(256), 0, st, W, x, nw, eps, logits, E, topk,
+  hipLaunchKernelGGL(k_router_topk<2048>, dim3((E + RT_WPB) / RT_WPB), dim3(RT_WPB * 64), 0, st, W, x, nw, eps, logits, E, topk,
                      idx, wts, sgate, counter);
   return 0;
 }

@@ -143,11 +143,12 @@ void or_exp_array(const float* x, float* y, size_t n) {
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* canonical fp32 reductions: 64 lanes, lane-strided chunks, then an xor butterfly */
+/* canonical fp32 reductions: 64 lanes, lane-strided chunks, then the ascending xor butterfly
+ * (step o = 1, 2, 4, ..., 32 combines a[l] and a[l ^ o]) */
 
 static float tree64(float* a) {
   float b[64];
-  for (int o = 32; o >= 1; o >>= 1) {
+  for (int o = 1; o <= 32; o <<= 1) {
     for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ o];
     memcpy(a, b, sizeof b);
   }

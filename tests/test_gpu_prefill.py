@@ -1,0 +1,279 @@
+"""GPU parity of the prefill path through the C ABI: grouping (exact), expert-grouped int4/fp8
+MFMA GEMM, fused int8 shared expert, combine, and the whole layer chain of
+Engine::moe_prefill (src/engine.rs:544-604) against the oracle.
+
+act is bf16 (kernels/drama.cu:879): it must match the oracle within one bf16 ulp (a last-bit
+rounding flip when the fp32 sums differ in their last bits).  fp32 outputs are checked with
+|gpu - ref| <= 1e-3 + 1e-3 |ref|; the down projection is checked on the GPU's own act so both
+sides multiply identical inputs."""
+import numpy as np
+import pytest
+
+import dramamoe as D
+import oracle as O
+import synth
+from helpers import assert_close, dev, host
+
+pytestmark = pytest.mark.gpu
+H, I = 2048, 512
+
+
+def t_i32(n):
+    import torch
+
+    return torch.zeros(n, dtype=torch.int32, device="cuda")
+
+
+def check_act(act, ract, what="act"):
+    """bf16 act within one rounding flip: |a - r| <= 2^-7 |r| + 1e-3 (1e-3 covers u ~ 0
+    cancellation, where fp32-vs-fp64 sums differ by ~1e-6 absolute)."""
+    a, r = synth.bf16_to_f32(act).astype(np.float64), synth.bf16_to_f32(ract).astype(np.float64)
+    bad = np.abs(a - r) > 2.0 ** -7 * np.abs(r) + 1e-3
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond one bf16 rounding flip"
+    return a, r
+
+
+def assert_close_with_flips(y, ref, Dmat, a, r, what):
+    """|y - ref| <= 1e-3 + 1e-3 |ref| + sum_j |D[n, j]| |a_j - r_j|: the tolerance plus exactly the
+    propagation of the act rounding flips observed (bf16 act, kernels/drama.cu:879)."""
+    extra = np.abs(a - r) @ np.abs(Dmat).T
+    err = np.abs(np.asarray(y, np.float64) - ref)
+    bad = err > 1e-3 + 1e-3 * np.abs(ref) + extra
+    assert not bad.any(), f"{what}: {int(bad.sum())}/{bad.size} outside tolerance + flip propagation"
+
+
+def bf16_ulp_diff(a, b):
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    sa, sb = a >> 15, b >> 15
+    # map sign-magnitude bf16 to a monotone integer line
+    ia = np.where(sa == 1, -(a & 0x7FFF), a & 0x7FFF)
+    ib = np.where(sb == 1, -(b & 0x7FFF), b & 0x7FFF)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("n,E,skew", [(2400, 256, False), (2400, 256, True), (1, 256, False), (8192, 256, False),
+                                      (17, 4, False), (0, 8, False)])
+def test_group_exact(n, E, skew):
+    import torch
+
+    rng = np.random.default_rng(n + E)
+    if skew:  # 10% of experts receive 50% of the pairs
+        hot = rng.choice(E, E // 10, replace=False)
+        idx = np.where(rng.random(n) < 0.5, rng.choice(hot, n), rng.integers(0, E, n)).astype(np.int32)
+    else:
+        idx = rng.integers(0, E, n).astype(np.int32)
+    rc, ro, rs = O.moe_group(idx, E)
+    counts, offsets, slot_of = t_i32(E), t_i32(E), t_i32(max(n, 1))
+    didx = dev(idx) if n else t_i32(1)
+    D.lib().dr_moe_group(D.ptr(didx), n, E, D.ptr(counts), D.ptr(offsets), D.ptr(slot_of), D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(counts), rc)
+    np.testing.assert_array_equal(host(offsets), ro)
+    if n:
+        np.testing.assert_array_equal(host(slot_of)[:n], rs)
+
+
+def test_count_and_permute_reference_abi():
+    """dr_moe_count + host scan + dr_moe_permute, the reference's sequence (src/engine.rs:564-578)."""
+    import torch
+
+    rng = np.random.default_rng(3)
+    rows, topk, E = 300, 8, 256
+    idx = rng.integers(0, E, rows * topk).astype(np.int32)
+    x = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    rc, ro, rs = O.moe_group(idx, E)
+    L = D.lib()
+    didx, counts = dev(idx), t_i32(E)
+    L.dr_moe_count(D.ptr(didx), rows * topk, D.ptr(counts), D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(counts), rc)
+    offsets, fill, slot_of = dev(ro), t_i32(E), t_i32(rows * topk)
+    dx = dev(x)
+    xp = torch.zeros(rows * topk * H, dtype=torch.int16, device="cuda")
+    L.dr_moe_permute(D.ptr(didx), rows, topk, D.ptr(offsets), D.ptr(fill), D.ptr(slot_of), D.ptr(dx), D.ptr(xp), H,
+                     D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(slot_of), rs)
+    np.testing.assert_array_equal(host(fill), rc)
+    xph = host(xp).view(np.uint16).reshape(rows * topk, H)
+    np.testing.assert_array_equal(xph[rs], x[np.arange(rows * topk) // topk])
+
+
+def grouped_inputs(seed, E, rows, topk, skew=False):
+    rng = np.random.default_rng(seed)
+    n = rows * topk
+    if skew:
+        hot = rng.choice(E, max(1, E // 10), replace=False)
+        idx = np.where(rng.random(n) < 0.5, rng.choice(hot, n), rng.integers(0, E, n)).astype(np.int32)
+    else:
+        idx = np.stack([rng.choice(E, topk, replace=False) for _ in range(rows)]).ravel().astype(np.int32)
+    counts, offsets, slot_of = O.moe_group(idx, E)
+    x = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    xp = np.empty((n, H), np.uint16)
+    xp[slot_of] = x[np.arange(n) // topk]
+    return idx, counts, offsets, slot_of, x, xp
+
+
+def run_prefill(Lh, xp, offsets, counts, fmt, kind):
+    import torch
+
+    E = Lh["E"]
+    n = xp.shape[0]
+    t = {k: dev(Lh[k]) for k in ("gu_q", "gu_s", "d_q", "d_s")}
+    dxp, doff, dcnt = dev(xp), dev(offsets), dev(counts)
+    act = torch.zeros(n * I, dtype=torch.int16, device="cuda")
+    yp = torch.zeros(n * H, dtype=torch.float32, device="cuda")
+    name = {("q4", "ref"): "dr_moe_prefill", ("q4", "cfg"): "dr_moe_prefill_bf16s",
+            ("fp8", "ref"): "dr_moe_prefill_fp8", ("fp8", "cfg"): "dr_moe_prefill_fp8_bf16s"}[(kind, fmt)]
+    getattr(D.lib(), name)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(dxp), D.ptr(doff),
+                           D.ptr(dcnt), D.ptr(act), D.ptr(yp), E, H, I, D.stream_ptr())
+    torch.cuda.synchronize()
+    return host(act).view(np.uint16).reshape(n, I), host(yp).reshape(n, H)
+
+
+def expert_dense(Lh, which, e):
+    """Dequantised [N, K] matrix of expert e via the oracle."""
+    kind = Lh["kind"]
+    q, s = Lh[which + "_q"][e], Lh[which + "_s"][e]
+    N = q.shape[0]
+    if kind == "q4":
+        return O.dequant_q4(np.ascontiguousarray(q), np.ascontiguousarray(s), Lh["sc_kind"], N, q.shape[1] * 2)
+    return O.dequant_fp8(np.ascontiguousarray(q), np.ascontiguousarray(s), Lh["sc_kind"], N, q.shape[1])
+
+
+@pytest.mark.parametrize("fmt,kind,skew", [("cfg", "q4", False), ("ref", "q4", False), ("cfg", "q4", True),
+                                           ("cfg", "fp8", False), ("ref", "fp8", False)])
+def test_grouped_gemm(fmt, kind, skew):
+    E, rows, topk = 24, 96, 8
+    Lh = synth.make_layer(40 + (kind == "fp8"), E=E, fmt=fmt, kind=kind)
+    idx, counts, offsets, slot_of, x, xp = grouped_inputs(41, E, rows, topk, skew)
+    act, yp = run_prefill(Lh, xp, offsets, counts, fmt, kind)
+    ract, ryp = O.moe_prefill_experts(Lh, xp, offsets, counts, E, H, I)
+    af, rf = check_act(act, ract)
+    print(f"counts min {counts.min()} max {counts.max()}; act rounding flips: {int((af != rf).sum())}/{af.size}")
+    for e in range(E):
+        if counts[e] == 0:
+            continue
+        sl = slice(offsets[e], offsets[e] + counts[e])
+        Dm = expert_dense(Lh, "d", e).astype(np.float64)
+        assert_close(yp[sl], af[sl] @ Dm.T, what=f"down expert {e} on the GPU's act")
+        assert_close_with_flips(yp[sl], ryp[sl].astype(np.float64), Dm, af[sl], rf[sl], f"expert {e} end to end")
+
+
+@pytest.mark.parametrize("fmt", ["cfg", "ref"])
+@pytest.mark.parametrize("rows", [300, 5])
+def test_shared_prefill(fmt, rows):
+    import torch
+
+    Lh = synth.make_layer(50, E=8, fmt=fmt)
+    rng = np.random.default_rng(51)
+    hn = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    t = {k: dev(Lh[k]) for k in ("sgu_q", "sgu_s", "sd_q", "sd_s")}
+    dhn = dev(hn)
+    act = torch.zeros(rows * I, dtype=torch.int16, device="cuda")
+    out = torch.zeros(rows * H, dtype=torch.float32, device="cuda")
+    name = "dr_moe_shared_prefill_bf16s" if fmt == "cfg" else "dr_moe_shared_prefill"
+    getattr(D.lib(), name)(D.ptr(t["sgu_q"]), D.ptr(t["sgu_s"]), D.ptr(t["sd_q"]), D.ptr(t["sd_s"]), D.ptr(dhn), rows,
+                           D.ptr(act), D.ptr(out), H, I, D.stream_ptr())
+    torch.cuda.synchronize()
+    ract, rout = O.shared_prefill(Lh, hn, rows, H, I)
+    a = host(act).view(np.uint16).reshape(rows, I)
+    af, rf = check_act(a, ract, "shared act")
+    sd = O.dequant_q8(Lh["sd_q"], Lh["sd_s"], Lh["sh_kind"], Lh["sh_group_d"], H, I).astype(np.float64)
+    o = host(out).reshape(rows, H)
+    assert_close(o, af @ sd.T, what="shared out on the GPU's act")
+    assert_close_with_flips(o, rout.astype(np.float64), sd, af, rf, "shared out end to end")
+
+
+def test_combine():
+    import torch
+
+    rng = np.random.default_rng(60)
+    rows, topk = 37, 8
+    n = rows * topk
+    x = rng.normal(0, 1, (rows, H)).astype(np.float32)
+    y = rng.normal(0, 1, (n, H)).astype(np.float32)
+    slot_of = rng.permutation(n).astype(np.int32)
+    wts = rng.random((rows, topk)).astype(np.float32)
+    sg = rng.normal(0, 2, rows).astype(np.float32)
+    sh = rng.normal(0, 1, (rows, H)).astype(np.float32)
+    dx = dev(x)
+    dy, dso, dw, dsg, dsh = dev(y), dev(slot_of), dev(wts), dev(sg), dev(sh)
+    D.lib().dr_moe_combine(D.ptr(dx), D.ptr(dy), D.ptr(dso), D.ptr(dw), D.ptr(dsg), D.ptr(dsh), rows, topk, H,
+                           D.stream_ptr())
+    torch.cuda.synchronize()
+    sig = 1 / (1 + np.exp(-sg.astype(np.float64)))
+    ref = x.astype(np.float64) + sig[:, None] * sh + np.einsum("rk,rkc->rc", wts.astype(np.float64),
+                                                               y[slot_of.reshape(rows, topk)].astype(np.float64))
+    assert_close(host(dx).reshape(rows, H), ref, rtol=1e-5, atol=1e-5, what="combine")
+
+
+@pytest.mark.parametrize("fmt", ["cfg", "ref"])
+def test_prefill_layer_chain(fmt):
+    """router GEMM -> top-k -> shared -> group -> gather -> grouped GEMM -> combine (E = 256)."""
+    import torch
+
+    E, rows, topk = 256, 300, 8
+    Lh = synth.make_layer(70, E=E, fmt=fmt)
+    rng = np.random.default_rng(71)
+    hn = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    x0 = rng.normal(0, 1, (rows, H)).astype(np.float32)
+    L, sp = D.lib(), D.stream_ptr()
+    t = {k: dev(Lh[k]) for k in ("router", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")}
+    dhn, dx = dev(hn), dev(x0)
+    logits = torch.zeros(rows * (E + 1), dtype=torch.float32, device="cuda")
+    idx, wts, sg = t_i32(rows * topk), torch.zeros(rows * topk, device="cuda"), torch.zeros(rows, device="cuda")
+    h = np.zeros(1, np.uint64)
+    L.dr_cublas_create(h.ctypes.data, sp)
+    L.dr_gemm(int(h[0]), D.ptr(dhn), D.ptr(t["router"]), D.ptr(logits), rows, E + 1, H, 0.0)
+    L.dr_moe_topk(D.ptr(logits), rows, E, topk, E + 1, D.ptr(idx), D.ptr(wts), D.ptr(sg), sp)
+    sact = torch.zeros(rows * I, dtype=torch.int16, device="cuda")
+    sh = torch.zeros(rows * H, device="cuda")
+    shname = "dr_moe_shared_prefill_bf16s" if fmt == "cfg" else "dr_moe_shared_prefill"
+    getattr(L, shname)(D.ptr(t["sgu_q"]), D.ptr(t["sgu_s"]), D.ptr(t["sd_q"]), D.ptr(t["sd_s"]), D.ptr(dhn), rows,
+                       D.ptr(sact), D.ptr(sh), H, I, sp)
+    counts, offsets, slot_of = t_i32(E), t_i32(E), t_i32(rows * topk)
+    L.dr_moe_group(D.ptr(idx), rows * topk, E, D.ptr(counts), D.ptr(offsets), D.ptr(slot_of), sp)
+    xp = torch.zeros(rows * topk * H, dtype=torch.int16, device="cuda")
+    L.dr_moe_gather_rows(D.ptr(slot_of), rows, topk, D.ptr(dhn), D.ptr(xp), H, sp)
+    act = torch.zeros(rows * topk * I, dtype=torch.int16, device="cuda")
+    yp = torch.zeros(rows * topk * H, device="cuda")
+    pname = "dr_moe_prefill_bf16s" if fmt == "cfg" else "dr_moe_prefill"
+    getattr(L, pname)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(xp), D.ptr(offsets),
+                      D.ptr(counts), D.ptr(act), D.ptr(yp), E, H, I, sp)
+    L.dr_moe_combine(D.ptr(dx), D.ptr(yp), D.ptr(slot_of), D.ptr(wts), D.ptr(sg), D.ptr(sh), rows, topk, H, sp)
+    torch.cuda.synchronize()
+    # routing: bit-exact against the oracle's canonical GEMM + softmax/top-k
+    rl = O.router_logits_rows(hn, Lh["router"], rows, E + 1, H)
+    ri, rw, rs = O.moe_topk(rl, rows, E, topk, E + 1)
+    np.testing.assert_array_equal(host(logits).reshape(rows, E + 1).view(np.uint32), rl.view(np.uint32))
+    np.testing.assert_array_equal(host(idx), ri)
+    np.testing.assert_array_equal(host(wts).view(np.uint32), rw.view(np.uint32))
+    rc, ro, rso = O.moe_group(ri, E)
+    np.testing.assert_array_equal(host(counts), rc)
+    np.testing.assert_array_equal(host(slot_of), rso)
+    ref = O.moe_prefill_layer(Lh, hn, rows, ri, rw, rs, x0, H, I, topk).astype(np.float64)
+    # intermediates of the oracle, to bound the effect of bf16 act rounding flips
+    n = rows * topk
+    xpr = np.empty((n, H), np.uint16)
+    xpr[rso] = hn[np.arange(n) // topk]
+    ract, _ = O.moe_prefill_experts(Lh, xpr, ro, rc, E, H, I)
+    rsact, _ = O.shared_prefill(Lh, hn, rows, H, I)
+    af, rf = check_act(host(act).view(np.uint16).reshape(n, I), ract, "routed act")
+    saf, srf = check_act(host(sact).view(np.uint16).reshape(rows, I), rsact, "shared act")
+    extra_slot = np.zeros((n, H))
+    for e in np.nonzero(rc)[0]:
+        sl = slice(ro[e], ro[e] + rc[e])
+        d = np.abs(af[sl] - rf[sl])
+        if d.any():
+            extra_slot[sl] = d @ np.abs(expert_dense(Lh, "d", e).astype(np.float64)).T
+    sd = O.dequant_q8(Lh["sd_q"], Lh["sd_s"], Lh["sh_kind"], Lh["sh_group_d"], H, I).astype(np.float64)
+    sig = 1 / (1 + np.exp(-rs.astype(np.float64)))
+    extra = sig[:, None] * (np.abs(saf - srf) @ np.abs(sd).T)
+    extra += np.einsum("rk,rkc->rc", rw.reshape(rows, topk).astype(np.float64), extra_slot[rso.reshape(rows, topk)])
+    got = host(dx).reshape(rows, H).astype(np.float64)
+    bad = np.abs(got - ref) > 1e-3 + 1e-3 * np.abs(ref) + extra
+    print(f"act flips routed {int((af != rf).sum())}, shared {int((saf != srf).sum())}; "
+          f"max |err| {np.abs(got - ref).max():.2e}")
+    assert not bad.any(), f"prefill layer output: {int(bad.sum())} outside tolerance + flip propagation"

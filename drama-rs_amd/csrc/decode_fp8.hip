@@ -1,0 +1,246 @@
+// Batch-1 decode MoE with block-FP8 (OCP e4m3) routed experts (reference:
+// kernels/drama.cu:602-742, src/ffi.rs:47-51).  Same structure as the int4 decode:
+//   gate_up: a 2048-byte e4m3 row is two 16-byte loads per lane (bytes [16 l, 16 l + 16) and
+//            [1024 + 16 l, ...)), the layout of the int8 shared rows, so routed and shared
+//            blocks stage x̂ identically; e4m3 -> f32 with v_cvt_pk_f32_fp8 (exact);
+//   down:    one output row gathers 8 expert rows of 512 bytes: 4 loads per lane, load i
+//            covering experts 2 i (lanes 0-31) and 2 i + 1 (lanes 32-63), plus 8 bytes of the
+//            int8 shared row.
+// One scale per 128 x 128 block (f32 scale_inv in the reference layout, bf16 in the
+// benchmark configuration); every 16-element lane chunk lies inside one block.
+#include "common.hpp"
+
+using namespace drm;
+
+namespace {
+
+constexpr int H8 = 2048, I8 = 512, TOPK8 = 8;
+constexpr int G8_WPB = 4, G8_PPW = 1;  // gate_up: waves per block, (gate, up) pairs per wave
+constexpr int G8_NB_ROUTED = TOPK8 * I8 / (G8_WPB * G8_PPW);
+constexpr int G8_NB_SHARED = I8 / G8_WPB;
+constexpr int D8_WPB = 4, D8_RPW = 2;
+
+template <int SF>
+DEV float blk_scale(const void* S, size_t i) {
+  return SF ? bf16f(reinterpret_cast<const uint16_t*>(S)[i]) : reinterpret_cast<const float*>(S)[i];
+}
+
+// sum_{i<16} e4m3(w bytes) * x[i]
+DEV float dot16_fp8(const uint4& w, const float* x, float acc) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], true);
+    acc = __builtin_fmaf(lo[0], x[4 * d + 0], acc);
+    acc = __builtin_fmaf(lo[1], x[4 * d + 1], acc);
+    acc = __builtin_fmaf(hi[0], x[4 * d + 2], acc);
+    acc = __builtin_fmaf(hi[1], x[4 * d + 3], acc);
+  }
+  return acc;
+}
+
+DEV float dot16_u8b(const uint4& w, const float* x, float acc) {
+  acc = dot4_u8b(w.x, x, acc);
+  acc = dot4_u8b(w.y, x + 4, acc);
+  acc = dot4_u8b(w.z, x + 8, acc);
+  return dot4_u8b(w.w, x + 12, acc);
+}
+
+template <int H>
+DEV void stage_xn16(const float* __restrict__ x, const float* __restrict__ nw, float eps, float4* xs) {
+  __shared__ float red[4];
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  constexpr int PER = H / 4 / 256;
+  float4 v[PER], w[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = x4[threadIdx.x + 256 * i];
+  if (nw) {
+    const float4* n4 = reinterpret_cast<const float4*>(nw);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) w[i] = n4[threadIdx.x + 256 * i];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = wave_sum(ss);
+    if (lane_id() == 0) red[wave_id()] = ss;
+    __syncthreads();
+    const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      v[i] = make_float4(v[i].x * inv * w[i].x, v[i].y * inv * w[i].y, v[i].z * inv * w[i].z, v[i].w * inv * w[i].w);
+  }
+  // float4 f -> lane (f & 255) >> 2 of part f >> 8, slot i = f & 3
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    xs[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = v[i];
+  }
+  __syncthreads();
+}
+
+template <int SF, class SH>
+__global__ void __launch_bounds__(256)
+    k_moe_gate_up_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
+                      const uint16_t* __restrict__ shs, const float* __restrict__ x, const int* __restrict__ idx,
+                      float* __restrict__ act, const float* __restrict__ nw, float eps) {
+  constexpr int H = H8, I = I8;
+  __shared__ float4 xs[H / 4];
+  const int lane = lane_id(), wave = wave_id();
+  const bool routed = blockIdx.x < G8_NB_ROUTED;
+  int k, j;
+  const uint8_t *rg, *ru;
+  float sg0, sg1, su0, su1;
+  if (routed) {
+    constexpr int BPE = G8_NB_ROUTED / TOPK8;
+    k = blockIdx.x / BPE;
+    j = (blockIdx.x % BPE) * G8_WPB + wave;
+    const size_t e = (size_t)idx[k];
+    const uint8_t* w = W + e * (2 * I) * H;
+    rg = w + (size_t)j * H + lane * 16;
+    ru = w + (size_t)(I + j) * H + lane * 16;
+    const size_t sb = e * (size_t)(2 * I / 128) * (H / 128);
+    sg0 = blk_scale<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + (lane >> 3));
+    sg1 = blk_scale<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + 8 + (lane >> 3));
+    su0 = blk_scale<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + (lane >> 3));
+    su1 = blk_scale<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + 8 + (lane >> 3));
+  } else {
+    k = TOPK8;
+    j = (blockIdx.x - G8_NB_ROUTED) * G8_WPB + wave;
+    rg = reinterpret_cast<const uint8_t*>(shq) + (size_t)j * H + lane * 16;
+    ru = reinterpret_cast<const uint8_t*>(shq) + (size_t)(I + j) * H + lane * 16;
+    sg0 = SH::scale(shs, j, lane * 16, H), sg1 = SH::scale(shs, j, 1024 + lane * 16, H);
+    su0 = SH::scale(shs, I + j, lane * 16, H), su1 = SH::scale(shs, I + j, 1024 + lane * 16, H);
+  }
+  const uint4 g0 = ld16(rg), g1 = ld16(rg + 1024), u0 = ld16(ru), u1 = ld16(ru + 1024);
+  stage_xn16<H>(x, nw, eps, xs);
+  float xa[16], xb[16], sa = 0.f, sb = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = xs[i * 64 + lane], w = xs[256 + i * 64 + lane];
+    xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+    xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+    sa += (v.x + v.y) + (v.z + v.w);
+    sb += (w.x + w.y) + (w.z + w.w);
+  }
+  float g, u;
+  if (routed) {
+    g = sg0 * dot16_fp8(g0, xa, 0.f) + sg1 * dot16_fp8(g1, xb, 0.f);
+    u = su0 * dot16_fp8(u0, xa, 0.f) + su1 * dot16_fp8(u1, xb, 0.f);
+  } else {
+    g = sg0 * (dot16_u8b(g0, xa, 0.f) - 128.f * sa) + sg1 * (dot16_u8b(g1, xb, 0.f) - 128.f * sb);
+    u = su0 * (dot16_u8b(u0, xa, 0.f) - 128.f * sa) + su1 * (dot16_u8b(u1, xb, 0.f) - 128.f * sb);
+  }
+  g = wave_sum(g);
+  u = wave_sum(u);
+  if (lane == 0) act[k * I + j] = silu(g) * u;
+}
+
+template <int SF, class SH>
+__global__ void __launch_bounds__(256)
+    k_moe_down_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
+                   const uint16_t* __restrict__ shs, const float* __restrict__ act, const int* __restrict__ idx,
+                   const float* __restrict__ wts, const float* __restrict__ sgate, const float* res, float* y,
+                   uint16_t* yb, const char* pf, size_t pf_bytes) {
+  constexpr int H = H8, I = I8;
+  __shared__ float4 as[(TOPK8 + 1) * I / 4];
+  const int lane = lane_id(), wave = wave_id();
+  const int half = lane >> 5, cc = lane & 31;
+  size_t e[4];
+  float w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) e[i] = (size_t)idx[2 * i + half], w[i] = wts[2 * i + half];
+  const int n0 = (blockIdx.x * D8_WPB + wave) * D8_RPW;
+  uint4 q[D8_RPW][4];
+  float sc[D8_RPW][4];
+  uint2 qs[D8_RPW];
+  float ss[D8_RPW];
+#pragma unroll
+  for (int r = 0; r < D8_RPW; ++r) {
+    const size_t n = (size_t)(n0 + r);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q[r][i] = ld16(W + (e[i] * H + n) * I + cc * 16);
+      sc[r][i] = blk_scale<SF>(S, (e[i] * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
+    }
+    qs[r] = ld8(shq + n * I + lane * 8);
+    ss[r] = SH::scale(shs, n, lane * 8, I);
+  }
+  const float sgv = sigmoid(sgate[0]);
+  // routed act: lane slice of load i = act[1024 i + 16 l .. + 16) -> 4 float4 per part of 256
+  const float4* a4 = reinterpret_cast<const float4*>(act);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    as[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = a4[f];
+  }
+  if (threadIdx.x < 128) {
+    const int f = threadIdx.x;
+    as[1024 + (f & 1) * 64 + (f >> 1)] = a4[1024 + f];
+  }
+  __syncthreads();
+  float xa[4][16], xc[8], sumc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4 v = as[256 * i + t * 64 + lane];
+      xa[i][4 * t] = v.x, xa[i][4 * t + 1] = v.y, xa[i][4 * t + 2] = v.z, xa[i][4 * t + 3] = v.w;
+    }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float4 v = as[1024 + t * 64 + lane];
+    xc[4 * t] = v.x, xc[4 * t + 1] = v.y, xc[4 * t + 2] = v.z, xc[4 * t + 3] = v.w;
+    sumc += (v.x + v.y) + (v.z + v.w);
+  }
+#pragma unroll
+  for (int r = 0; r < D8_RPW; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc += w[i] * sc[r][i] * dot16_fp8(q[r][i], xa[i], 0.f);
+    float dc = dot4_u8b(qs[r].x, xc, 0.f);
+    dc = dot4_u8b(qs[r].y, xc + 4, dc);
+    acc += sgv * ss[r] * (dc - 128.f * sumc);
+    acc = wave_sum(acc);
+    const int n = n0 + r;
+    if (lane == 0) {
+      const float out = res[n] + acc;
+      y[n] = out;
+      if (yb) yb[n] = to_bf16(out);
+    }
+  }
+  warm_range(pf, pf_bytes);
+}
+
+template <int SF, class SH>
+int launch_decode_fp8(const uint8_t* gu_w, const void* gu_s, const uint8_t* d_w, const void* d_s, const int8_t* sgu_q,
+                      const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s, const float* x, const int* idx,
+                      const float* wts, const float* sgate, const float* res, float* act, float* y, uint16_t* yb, int H,
+                      int I, int topk, const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st) {
+  if (H != H8 || I != I8 || topk != TOPK8) return -1;
+  hipLaunchKernelGGL((k_moe_gate_up_fp8<SF, SH>), dim3(G8_NB_ROUTED + G8_NB_SHARED), dim3(256), 0, st, gu_w, gu_s,
+                     sgu_q, sgu_s, x, idx, act, nw, eps);
+  hipLaunchKernelGGL((k_moe_down_fp8<SF, SH>), dim3(H8 / (D8_WPB * D8_RPW)), dim3(256), 0, st, d_w, d_s, sd_q, sd_s,
+                     act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
+  return 0;
+}
+
+}  // namespace
+
+API int dr_moe_decode_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                          const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                          const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                          float* act, float* y, int H, int I, int topk, const float* nw, float eps, const char* pf,
+                          size_t pf_bytes, hipStream_t st) {
+  return launch_decode_fp8<0, Q8G128F16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
+                                         y, nullptr, H, I, topk, nw, eps, pf, pf_bytes, st);
+}
+
+API int dr_moe_decode_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, const uint8_t* d_w, const uint16_t* d_s,
+                                const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                                const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                                float* act, float* y, uint16_t* yb, int H, int I, int topk, const float* nw, float eps,
+                                const char* pf, size_t pf_bytes, hipStream_t st) {
+  return launch_decode_fp8<1, Q8RowBF16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
+                                         y, yb, H, I, topk, nw, eps, pf, pf_bytes, st);
+}

@@ -157,3 +157,57 @@ def test_gemv_q4_config1(N, K):
     torch.cuda.synchronize()
     assert_close(host(y), ref, what="gemv y")
     assert np.abs(host(yb).view(np.uint16).astype(np.int32) - synth.f32_to_bf16(ref).astype(np.int32)).max() <= 1
+
+
+@pytest.mark.parametrize("fmt", ["ref", "cfg"])
+def test_decode_fp8_matches_oracle(fmt):
+    """Block-FP8 e4m3 experts (kernels/drama.cu:602-742): f32 scale_inv (reference) or bf16 scales."""
+    import torch
+
+    E = 32
+    Lh = layer(13, E, fmt, kind="fp8")
+    dl = DevLayer(Lh)
+    rng = np.random.default_rng(14)
+    x = rng.normal(0, 1, 2048).astype(np.float32)
+    res = rng.normal(0, 1, 2048).astype(np.float32)
+    _, idx, wts, sg = O.router_topk(Lh["router"], x, Lh["nw"], 1e-6, E, 8)
+    ract, ry = O.moe_decode(Lh, x, idx, wts, sg, res, 2048, 512, 8, nw=Lh["nw"], eps=1e-6)
+    L = D.lib()
+    act = torch.zeros(9 * 512, dtype=torch.float32, device="cuda")
+    dx, dr = dev(x), dev(res)
+    out = torch.empty(2048, dtype=torch.float32, device="cuda")
+    di, dw, ds = dev(idx.astype(np.int32)), dev(wts), dev(np.array([sg], np.float32))
+    args = [dl.p("gu_q"), dl.p("gu_s"), dl.p("d_q"), dl.p("d_s"), dl.p("sgu_q"), dl.p("sgu_s"), dl.p("sd_q"),
+            dl.p("sd_s"), D.ptr(dx), D.ptr(di), D.ptr(dw), D.ptr(ds), D.ptr(dr), D.ptr(act), D.ptr(out)]
+    if fmt == "ref":
+        L.dr_moe_decode_fp8(*args, 2048, 512, 8, dl.p("nw"), 1e-6, None, 0, D.stream_ptr())
+    else:
+        L.dr_moe_decode_fp8_bf16s(*args, None, 2048, 512, 8, dl.p("nw"), 1e-6, None, 0, D.stream_ptr())
+    torch.cuda.synchronize()
+    assert_close(host(act), ract, what="fp8 act")
+    assert_close(host(out), ry, what="fp8 y")
+
+
+def test_decode_prefetch_range_is_harmless():
+    """pf/pf_bytes only warm the cache: results equal a call without them."""
+    import torch
+
+    E = 16
+    Lh = layer(15, E, "cfg")
+    dl = DevLayer(Lh)
+    x = np.random.default_rng(16).normal(0, 1, 2048).astype(np.float32)
+    _, idx, wts, sg = O.router_topk(Lh["router"], x, Lh["nw"], 1e-6, E, 8)
+    outs = []
+    for pf in (None, dl.t["router"]):
+        act = torch.zeros(9 * 512, device="cuda")
+        dx = dev(x)
+        out = torch.empty(2048, device="cuda")
+        di, dw, ds = dev(idx), dev(wts), dev(np.array([sg], np.float32))
+        D.lib().dr_moe_decode_bf16s(dl.p("gu_q"), dl.p("gu_s"), dl.p("d_q"), dl.p("d_s"), dl.p("sgu_q"), dl.p("sgu_s"),
+                                    dl.p("sd_q"), dl.p("sd_s"), D.ptr(dx), D.ptr(di), D.ptr(dw), D.ptr(ds), D.ptr(dx),
+                                    D.ptr(act), D.ptr(out), None, 2048, 512, 8, dl.p("nw"), 1e-6,
+                                    D.ptr(pf) if pf is not None else None, pf.numel() * 2 if pf is not None else 0,
+                                    D.stream_ptr())
+        torch.cuda.synchronize()
+        outs.append(host(out))
+    np.testing.assert_array_equal(outs[0], outs[1])

@@ -33,6 +33,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-extra", action="store_true", help="skip configurations 1, 4 and 5")
     return ap.parse_args()
 
 
@@ -181,6 +182,21 @@ def main():
     lib.dr_graph_destroy(gexec)
     ok = bool(torch.isfinite(x).all().item())
 
+    # ---- the other benchmark configurations (single GEMV, prefill, FP8 and int8 dense)
+    extra = None
+    if not args.no_extra:
+        import benchcfg
+
+        extra = {}
+        for name, fn in (("cfg1_gemv_int4", lambda: benchcfg.config1_gemv(lib, st)),
+                         ("cfg4_prefill_int4", lambda: benchcfg.config4_prefill(lib, layers, st)),
+                         ("cfg5_fp8_and_int8", lambda: benchcfg.config5_fp8(lib, st))):
+            try:
+                extra[name] = fn()
+            except Exception as e:  # reported, never fatal for the headline
+                extra[name] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+
     # ---- CPU baseline: the oracle's decode layer on this host's cores (bounded sample)
     cpu = None
     if not args.no_cpu:
@@ -229,6 +245,7 @@ def main():
                      "bytes_per_step": bytes_step, "kernel": "whole decode step (router + gate_up + down per layer)"},
         "cpu_baseline": cpu,
         "parity": parity,
+        "configs": extra,
         "finite": ok,
         "setup_s": round(gen_s, 1),
     }

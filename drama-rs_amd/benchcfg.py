@@ -1,0 +1,234 @@
+"""Measurements of the benchmark configurations other than the headline 40-layer decode step
+(configurations 1, 4 and 5), used by bench.py.  Every timing is HIP events on the stream the
+kernels run on; weights are rotated over distinct copies wherever one launch would otherwise
+re-read data that fits in the 256 MB memory-side cache."""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+import dramamoe as D
+
+HBM = 8000.0  # GB/s
+H, I, E, TOPK = 2048, 512, 256, 8
+
+
+def bf16_bits(t):
+    return t.to(torch.bfloat16).view(torch.int16)
+
+
+def timed(fn, iters, st, warmup=3):
+    # inputs are generated on torch's default stream; the kernels run on st
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        fn(i)
+    st.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(iters):
+        fn(i)
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters  # ms
+
+
+def rec(us, nbytes, **kw):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out = {"us": round(us, 2), "bytes": int(nbytes), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM, 4)}
+    out.update(kw)
+    return out
+
+
+def config1_gemv(lib, st, iters=200):
+    """Single int4 GEMV 1024 x 2048, group 64, bf16 scale/min, bf16 x, bf16 + f32 out."""
+    N, K, R = 1024, 2048, 256
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randint(0, 256, (R, N, K // 2), generator=g, device="cuda", dtype=torch.uint8)
+    sc = torch.randn(R, N, K // 64, generator=g, device="cuda").abs() * 0.02 + 1e-4
+    mn = torch.randn(R, N, K // 64, generator=g, device="cuda") * 0.02
+    sm = torch.stack([bf16_bits(sc), bf16_bits(mn)], -1).contiguous()
+    del sc, mn
+    x = bf16_bits(torch.randn(K, generator=g, device="cuda"))
+    y = torch.empty(N, device="cuda")
+    yb = torch.empty(N, dtype=torch.int16, device="cuda")
+    sp = st.cuda_stream
+    P = D.ptr
+    qs, ss = q.stride(0), sm.stride(0) * 2
+
+    def f(i):
+        r = i % R
+        lib.dr_gemv_q4_bf16s(q.data_ptr() + r * qs, sm.data_ptr() + r * ss, P(x), P(y), P(yb), N, K, sp)
+
+    ms = timed(f, iters, st)
+    nbytes = N * K // 2 + N * (K // 64) * 4 + K * 2 + N * 6
+    return rec(ms * 1000, nbytes, shape=f"{N}x{K}", note="rotated over 256 distinct matrices; launch-bound")
+
+
+class Prefill:
+    """Buffers of one prefill layer call for `rows` rows (Engine::moe_prefill, src/engine.rs:544-604)."""
+
+    def __init__(self, rows, st):
+        z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
+        n = rows * TOPK
+        self.rows, self.n, self.st, self.sp = rows, n, st, st.cuda_stream
+        g = torch.Generator(device="cuda").manual_seed(21)
+        self.hn = bf16_bits(torch.randn(rows, H, generator=g, device="cuda"))
+        self.x = torch.randn(rows, H, generator=g, device="cuda")
+        self.logits = z(rows * (E + 1))
+        self.idx, self.wts, self.sg = z(n, torch.int32), z(n), z(rows)
+        self.sact, self.sh = z(rows * I, torch.int16), z(rows * H)
+        self.counts, self.offsets, self.slot_of = z(E, torch.int32), z(E, torch.int32), z(n, torch.int32)
+        self.xp, self.act, self.yp = z(n * H, torch.int16), z(n * I, torch.int16), z(n * H)
+        h = ctypes.c_void_p()
+        D.lib().dr_cublas_create(ctypes.byref(h), self.sp)
+        self.h = h.value
+
+    def router(self, lib, L):
+        P = D.ptr
+        lib.dr_gemm(self.h, P(self.hn), P(L["router"]), P(self.logits), self.rows, E + 1, H, 0.0)
+        lib.dr_moe_topk(P(self.logits), self.rows, E, TOPK, E + 1, P(self.idx), P(self.wts), P(self.sg), self.sp)
+
+    def experts(self, lib, L, fp8=False):
+        P, sp = D.ptr, self.sp
+        lib.dr_moe_shared_prefill_bf16s(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(self.hn), self.rows,
+                                        P(self.sact), P(self.sh), H, I, sp)
+        lib.dr_moe_group(P(self.idx), self.n, E, P(self.counts), P(self.offsets), P(self.slot_of), sp)
+        lib.dr_moe_gather_rows(P(self.slot_of), self.rows, TOPK, P(self.hn), P(self.xp), H, sp)
+        f = lib.dr_moe_prefill_fp8_bf16s if fp8 else lib.dr_moe_prefill_bf16s
+        f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.xp), P(self.offsets), P(self.counts), P(self.act),
+          P(self.yp), E, H, I, sp)
+        lib.dr_moe_combine(P(self.x), P(self.yp), P(self.slot_of), P(self.wts), P(self.sg), P(self.sh), self.rows, TOPK,
+                           H, sp)
+
+    def layer_bytes(self, L, include_router=True):
+        hit = int((self.counts > 0).sum().item())
+        per_expert = sum(L[k].numel() * L[k].element_size() for k in ("gu_q", "gu_s", "d_q", "d_s")) // E
+        shared = sum(L[k].numel() * L[k].element_size() for k in ("sgu_q", "sgu_s", "sd_q", "sd_s"))
+        r, n = self.rows, self.n
+        acts = (r * H * 2 * 3          # hn read by router, shared and gather
+                + n * H * 2 * 2        # xp written and read
+                + n * I * 2 * 2        # act written and read
+                + n * H * 4 * 2        # yp written and read
+                + r * I * 2 * 2 + r * H * 4 * 2  # shared act / out
+                + r * H * 4 * 2)       # x read and written
+        return hit * per_expert + shared + (L["router"].numel() * 2 if include_router else 0) + acts, hit
+
+
+def config4_prefill(lib, layers, st, iters=40):
+    """300 token rows, top-8 of 256 (2400 pairs), rotated over the 40 resident layers."""
+    pf = Prefill(300, st)
+    nl = len(layers)
+
+    def full(i):
+        L = layers[i % nl]
+        pf.router(lib, L)
+        pf.experts(lib, L)
+
+    ms = timed(full, iters, st)
+    nbytes, hit = pf.layer_bytes(layers[0])
+    cnt = pf.counts.cpu()
+    uniform = rec(ms * 1000, nbytes, experts_hit=hit, rows_per_expert_max=int(cnt.max()), pairs=pf.n,
+                  note="router GEMM + top-k + shared + group + gather + grouped GEMM + combine")
+    # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
+    g = torch.Generator(device="cuda").manual_seed(31)
+    hot = torch.randperm(E, generator=g, device="cuda")[: E // 10]
+    pick_hot = torch.rand(pf.n, generator=g, device="cuda") < 0.5
+    idx = torch.where(pick_hot, hot[torch.randint(0, hot.numel(), (pf.n,), generator=g, device="cuda")],
+                      torch.randint(0, E, (pf.n,), generator=g, device="cuda")).to(torch.int32)
+    pf.idx.copy_(idx)
+    pf.wts.fill_(1.0 / TOPK)
+
+    def skewed(i):
+        pf.experts(lib, layers[i % nl])
+
+    ms2 = timed(skewed, iters, st)
+    nbytes2, hit2 = pf.layer_bytes(layers[0], include_router=False)
+    cnt2 = pf.counts.cpu()
+    skew = rec(ms2 * 1000, nbytes2, experts_hit=hit2, rows_per_expert_max=int(cnt2.max()),
+               note="skewed: 10% of experts get 50% of the pairs; routing given, no router GEMM")
+    return {"uniform": uniform, "skewed": skew}
+
+
+def make_fp8_layer(seed):
+    """256 e4m3 experts quantised from N(0, 0.02) with bf16 128 x 128 block scales."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    L = {"router": bf16_bits(torch.randn(E + 1, H, generator=g, device="cuda") * 0.02),
+         "nw": 1.0 + 0.1 * torch.randn(H, generator=g, device="cuda")}
+
+    def fp8(n, k):
+        q = torch.empty(E, n, k, dtype=torch.uint8, device="cuda")
+        s = torch.empty(E, n // 128, k // 128, dtype=torch.int16, device="cuda")
+        for e0 in range(0, E, 16):
+            w = torch.randn(16, n, k, generator=g, device="cuda") * 0.02
+            blk = w.view(16, n // 128, 128, k // 128, 128)
+            amax = blk.abs().amax(dim=(2, 4)).clamp_min(1e-12)
+            sb = (amax / 448.0).to(torch.bfloat16)
+            qv = (blk / sb.float()[:, :, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+            q[e0:e0 + 16] = qv.view(torch.uint8).view(16, n, k)
+            s[e0:e0 + 16] = sb.view(torch.int16)
+        return q, s
+
+    L["gu_q"], L["gu_s"] = fp8(2 * I, H)
+    L["d_q"], L["d_s"] = fp8(H, I)
+
+    def q8(n, k):
+        return (torch.randint(-127, 128, (n, k), generator=g, device="cuda", dtype=torch.int8),
+                bf16_bits((torch.randn(n, generator=g, device="cuda").abs() * 0.02 + 1e-4) / 73.0))
+
+    L["sgu_q"], L["sgu_s"] = q8(2 * I, H)
+    L["sd_q"], L["sd_s"] = q8(H, I)
+    return L
+
+
+def config5_fp8(lib, st, iters=100):
+    out = {}
+    L = make_fp8_layer(41)
+    sp, P = st.cuda_stream, D.ptr
+    z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
+    x = torch.randn(H, device="cuda")
+    logits, idx, wts, sg, counter, act = z(E + 1), z(TOPK, torch.int32), z(TOPK), z(1), z(4, torch.int32), z(9 * I)
+
+    def dec(i):
+        lib.dr_router_topk(P(L["router"]), P(x), P(L["nw"]), 1e-6, P(logits), E, TOPK, H, P(idx), P(wts), P(sg),
+                           P(counter), None, None, None, None, 0, 0, 0, 0, sp)
+        lib.dr_moe_decode_fp8_bf16s(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]),
+                                    P(L["sd_q"]), P(L["sd_s"]), P(x), P(idx), P(wts), P(sg), P(x), P(act), P(x), None,
+                                    H, I, TOPK, P(L["nw"]), 1e-6, None, 0, sp)
+
+    ms = timed(dec, iters, st)
+    per_expert = sum(L[k].numel() * L[k].element_size() for k in ("gu_q", "gu_s", "d_q", "d_s")) // E
+    shared = sum(L[k].numel() * L[k].element_size() for k in ("sgu_q", "sgu_s", "sd_q", "sd_s"))
+    b1 = L["router"].numel() * 2 + TOPK * per_expert + shared + 6 * H * 4 + 2 * 9 * I * 4
+    out["decode_batch1"] = rec(ms * 1000, b1, note="router + fp8 gate_up + down + int8 shared; x evolves per call")
+    # batch 4 through the grouped (prefill) path: union of up to 32 experts
+    pf = Prefill(4, st)
+
+    def b4(i):
+        pf.router(lib, L)
+        pf.experts(lib, L, fp8=True)
+
+    ms4 = timed(b4, iters, st)
+    nb4, hit = pf.layer_bytes(L)
+    out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, note="4 rows via the grouped MFMA path (bf16 act)")
+    del L
+    torch.cuda.empty_cache()
+    # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections
+    g = torch.Generator(device="cuda").manual_seed(51)
+    V = 151936
+    W = torch.randint(-127, 128, (V, H), generator=g, device="cuda", dtype=torch.int8)
+    S = bf16_bits(torch.rand(V, generator=g, device="cuda") * 1e-3 + 1e-5)
+    y = z(V)
+    xs = torch.randn(H, device="cuda")
+    msl = timed(lambda i: lib.dr_gemv_q8_bf16s(P(W), P(S), P(xs), None, P(y), V, H, None, 0.0, sp), 20, st)
+    out["lm_head_int8"] = rec(msl * 1000, V * H + V * 2 + H * 4 + V * 4, shape=f"{V}x{H}")
+    del W, S, y
+    R = 64
+    Wp = torch.randint(-127, 128, (R, H, H), generator=g, device="cuda", dtype=torch.int8)
+    Sp = bf16_bits(torch.rand(R, H, generator=g, device="cuda") * 1e-3 + 1e-5)
+    yp = z(H)
+    mp = timed(lambda i: lib.dr_gemv_q8_bf16s(Wp.data_ptr() + (i % R) * H * H, Sp.data_ptr() + (i % R) * H * 2, P(xs),
+                                               None, P(yp), H, H, None, 0.0, sp), 200, st)
+    out["proj_int8_2048"] = rec(mp * 1000, H * H + H * 2 + H * 8, shape="2048x2048",
+                                note="rotated over 64 matrices; launch-bound")
+    return out

@@ -96,13 +96,19 @@ DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* m
     z = z + ex[j];
   }
   z = wave_sum(z);
+  // Selection keys: p for valid experts, -1 for a NaN probability, -2 once picked, -3 for
+  // padding slots e >= E; the running best starts at -4.  Every round therefore picks a
+  // distinct expert below E (topk <= E), whatever the logits hold.
   float p[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = (lane + WAVE * j) < E ? ex[j] / z : -1.f;
+  for (int j = 0; j < 4; ++j) {
+    const float q = ex[j] / z;
+    p[j] = (lane + WAVE * j) < E ? (q != q ? -1.f : q) : -3.f;
+  }
   float total = 0.f, w = 0.f;
   int id = 0;
   for (int k = 0; k < topk; ++k) {
-    float bv = -2.f;
+    float bv = -4.f;
     int bi = 1 << 30;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -110,7 +116,7 @@ DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* m
     wave_argmax(bv, bi);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (lane + WAVE * j == bi) p[j] = -1.f;
+      if (lane + WAVE * j == bi) p[j] = -2.f;
     total = total + bv;
     if (lane == k) w = bv, id = bi;
   }

@@ -223,17 +223,22 @@ int or_softmax_topk(const float* l, int E, int topk, int* idx, float* wts) {
     a[ln] = s;
   }
   const float z = tree64(a);
-  for (int e = 0; e < 256; ++e) p[e] = e < E ? ex[e] / z : -1.f;
+  /* selection keys: p, -1 for a NaN probability, -2 once picked; the best starts at -4, so
+   * every round picks a distinct expert below E whatever the logits hold */
+  for (int e = 0; e < 256; ++e) {
+    const float q = ex[e] / z;
+    p[e] = e < E ? (q != q ? -1.f : q) : -3.f;
+  }
   float total = 0.f;
   for (int k = 0; k < topk; ++k) {
-    int bi = -1;
-    float bv = -2.f;
+    int bi = 0;
+    float bv = -4.f;
     for (int e = 0; e < E; ++e)
       if (p[e] > bv) bv = p[e], bi = e; /* strict > keeps the lowest index on ties */
     idx[k] = bi;
     wts[k] = bv;
     total = total + bv;
-    p[bi] = -1.f;
+    p[bi] = -2.f;
   }
   for (int k = 0; k < topk; ++k) wts[k] = wts[k] / total;
   return 0;

@@ -117,3 +117,26 @@ def test_gemm_canonical_bit_exact(M, N, K):
     L.dr_gemm(int(h[0]), D.ptr(dA), D.ptr(dWt), D.ptr(C), M, N, K, 0.0)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(host(C)).reshape(M, N), bits(ref))
+
+
+def test_router_nan_input_selects_valid_experts():
+    """A NaN in x makes every probability NaN; the selected experts must still be distinct
+    and below E (the decode kernels index expert weights with them)."""
+    import torch
+
+    E = 256
+    W, x, nw = _router_case(7, E, True)
+    x[5] = np.nan
+    rl, ri, rw, rs = O.router_topk(W, x, nw, 1e-6, E, 8)
+    dW, dx, dnw = dev(W), dev(x), dev(nw)
+    logits = torch.empty(E + 1, dtype=torch.float32, device="cuda")
+    idx = torch.full((8,), -7, dtype=torch.int32, device="cuda")
+    wts = torch.empty(8, dtype=torch.float32, device="cuda")
+    sg = torch.empty(1, dtype=torch.float32, device="cuda")
+    counter = torch.zeros(4, dtype=torch.int32, device="cuda")
+    D.lib().dr_router_topk(D.ptr(dW), D.ptr(dx), D.ptr(dnw), 1e-6, D.ptr(logits), E, 8, 2048, D.ptr(idx), D.ptr(wts),
+                           D.ptr(sg), D.ptr(counter), None, None, None, None, 0, 0, 0, 0, D.stream_ptr())
+    torch.cuda.synchronize()
+    gi = host(idx)
+    assert len(set(gi.tolist())) == 8 and gi.min() >= 0 and gi.max() < E
+    np.testing.assert_array_equal(gi, ri)

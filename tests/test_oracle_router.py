@@ -128,3 +128,15 @@ def test_group_invariants_and_brute_force():
         expect = np.empty(n, np.int32)
         expect[perm] = np.arange(n)
         np.testing.assert_array_equal(slot_of, expect)
+
+
+def test_softmax_topk_nan_logits_pick_distinct_valid_experts():
+    """NaN probabilities rank below every real one, never leave [0, E) and never repeat."""
+    for E in (256, 16, 8):
+        l = np.full(E, np.nan, np.float32)
+        idx, w = O.softmax_topk(l, E, 8)
+        np.testing.assert_array_equal(idx, np.arange(8))
+        l = np.random.default_rng(E).normal(0, 1, E).astype(np.float32)
+        l[[1, 3]] = np.nan  # one NaN poisons the max and the sum: every p is NaN
+        idx, w = O.softmax_topk(l, E, 8)
+        assert len(set(idx.tolist())) == 8 and idx.min() >= 0 and idx.max() < E

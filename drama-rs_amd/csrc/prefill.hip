@@ -5,21 +5,24 @@
 // gate_up: act[t] = bf16(silu(G_e . x_t) * (U_e . x_t)); down: y[t] = D_e . act_t (fp32).
 //
 // One wave owns a 16-row tile of weight rows (for gate_up: 16 gate rows and the 16 matching
-// up rows) and computes it against up to 64 tokens of its expert with
-// v_mfma_f32_16x16x32_bf16: A = weights (16 x 32), B = tokens (32 x 16), D = 16 x 16 fp32.
+// up rows) and computes it against one 16-token pass of its expert with
+// v_mfma_f32_16x16x32_bf16: A = tokens (16 x 32), B = weights (32 x 16), D = 16 x 16 fp32, so
+// the four D values of a lane share one weight row and the per-row scale stays in a register.
+// Passes of one expert are spread over grid z; the 16 tokens of a pass sit in LDS (K x 16 bf16).
 // Weights are dequantised exactly in registers: an int4 nibble q becomes the bf16 value
 // 128 + q (bit pattern 0x4300 | q), an int8 or fp8 value converts to bf16 exactly.  Each MFMA
 // stays inside one scale group, so per group g the fp32 product sum acc_g is rescaled:
 //   int4:  out += s_g acc_g + (m_g - 128 s_g) X_g,  X_g = sum of the group's inputs
 //   int8 / fp8:  out += s_g acc_g  (one scale per 128 inputs, or one per row at the end)
 // which is w = q s + m applied after exact integer x bf16 products: the same values as
-// dequantise-then-fp32, accumulated in fp32.
+// dequantise-then-fp32, accumulated in fp32.  X_g comes from one more MFMA with bf16 ones.
 //
 // Lane l of a wave holds, for MFMA step s (two per 64-wide group G), weight row (l % 16) and
 // the 8 inputs k = 64 G + 16 (l / 16) + 8 s + perm(t), t = 0..7, where perm = 0 4 1 5 2 6 3 7
 // is the order in which the nibble masking (w >> 4 j) & 0x000f000f produces bf16 pairs.  The
-// token tile in LDS is stored in the same permuted order, so each B fragment is one 16-byte
-// LDS read.
+// token tile in LDS is stored in the same permuted order, 16-byte chunk b of token t at
+// b ^ (t % 16) so the 16 token rows of one read spread over all banks; each A fragment is one
+// 16-byte LDS read.  Weight loads run two steps ahead of the MFMAs.
 #include "common.hpp"
 
 using namespace drm;
@@ -30,8 +33,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int PF_WPB = 8;     // waves per block
-constexpr int PF_TOK = 64;    // tokens per pass (4 token tiles of 16)
-constexpr int PF_KC = 256;    // inputs per LDS chunk (4 groups of 64)
+constexpr int PF_TOK = 16;    // tokens per pass (one MFMA tile)
+constexpr int PF_ZPASS = 4;   // passes of one expert that run concurrently (grid z)
 constexpr int PF_MAXE = 256;  // experts
 
 DEV f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
@@ -54,10 +57,12 @@ struct FmtQ4 {
     a0 = make_uint4((raw.x & m) | b, ((raw.x >> 4) & m) | b, ((raw.x >> 8) & m) | b, ((raw.x >> 12) & m) | b);
     a1 = make_uint4((raw.y & m) | b, ((raw.y >> 4) & m) | b, ((raw.y >> 8) & m) | b, ((raw.y >> 12) & m) | b);
   }
-  // (scale, min) of row n, group G
-  static DEV float2 scale(const void* S, size_t n, int G, int K) {
-    return SC::pair(reinterpret_cast<const uint32_t*>(S)[n * (K / 64) + G]);
+  // (scale, min) of row n, group G: raw word, then decoded
+  static DEV uint32_t scale_raw(const void* S, size_t n, int G, int K) {
+    return reinterpret_cast<const uint32_t*>(S)[n * (K / 64) + G];
   }
+  static DEV float2 scale_val(uint32_t w) { return SC::pair(w); }
+  static DEV float2 scale(const void* S, size_t n, int G, int K) { return scale_val(scale_raw(S, n, G, K)); }
 };
 
 // element order inside an 8-element fragment: perm = 0 4 1 5 2 6 3 7
@@ -80,9 +85,11 @@ struct FmtQ8 {
     a0 = frag(raw.x, raw.y);
     a1 = frag(raw.z, raw.w);
   }
-  static DEV float2 scale(const void* S, size_t n, int G, int K) {
-    return make_float2(SH::scale(reinterpret_cast<const uint16_t*>(S), n, G * 64, K), 0.f);
+  static DEV uint32_t scale_raw(const void* S, size_t n, int G, int K) {
+    return __float_as_uint(SH::scale(reinterpret_cast<const uint16_t*>(S), n, G * 64, K));
   }
+  static DEV float2 scale_val(uint32_t w) { return make_float2(__uint_as_float(w), 0.f); }
+  static DEV float2 scale(const void* S, size_t n, int G, int K) { return scale_val(scale_raw(S, n, G, K)); }
 };
 
 // fp8 e4m3 (OCP), one scale per 128 x 128 block; SF: 0 = f32 scales, 1 = bf16 scales
@@ -106,10 +113,12 @@ struct FmtFP8 {
     a1 = frag(raw.z, raw.w);
   }
   // scale of row n, 64-group G: block (n / 128, G / 2); S points at this expert's blocks
-  static DEV float2 scale(const void* S, size_t n, int G, int K) {
+  static DEV uint32_t scale_raw(const void* S, size_t n, int G, int K) {
     const size_t i = (n >> 7) * (size_t)(K / 128) + (G >> 1);
-    return make_float2(SF ? bf16f(reinterpret_cast<const uint16_t*>(S)[i]) : reinterpret_cast<const float*>(S)[i], 0.f);
+    return SF ? (uint32_t)reinterpret_cast<const uint16_t*>(S)[i] << 16 : reinterpret_cast<const uint32_t*>(S)[i];
   }
+  static DEV float2 scale_val(uint32_t w) { return make_float2(__uint_as_float(w), 0.f); }
+  static DEV float2 scale(const void* S, size_t n, int G, int K) { return scale_val(scale_raw(S, n, G, K)); }
 };
 
 template <class F>
@@ -127,160 +136,160 @@ struct Raw<FmtFP8<SF>> {
   using T = uint4;
 };
 
-// Stage tokens [t0, t0 + 64) x inputs [kc, kc + PF_KC) of a bf16 row matrix into LDS in the
-// permuted fragment order, zero-filling tokens >= ntok; xsum[t][gi] = sum of the 64 inputs
-// of group gi for token t (fp32).
-DEV void stage_tokens(const uint16_t* __restrict__ X, size_t row0, int ntok, int K, int kc, uint4* xs, float* xsum) {
-  constexpr int BLK = PF_TOK * PF_KC / 8;  // 16-byte blocks
-  for (int b = threadIdx.x; b < BLK; b += PF_WPB * 64) {
-    const int t = b / (PF_KC / 8), r = b % (PF_KC / 8);
+// Stage tokens [row0, row0 + ntok) x all K inputs of a bf16 row matrix into LDS in the
+// permuted fragment order: 16-byte block r of token t at t * K / 8 + (r ^ t), the xor spreading the 16
+// tokens of one read over distinct LDS banks; rows beyond ntok are zero.
+DEV void stage_tokens(const uint16_t* __restrict__ X, size_t row0, int ntok, int K, uint4* xs) {
+  const int blk = PF_TOK * K / 8;
+  for (int b = threadIdx.x; b < blk; b += PF_WPB * 64) {
+    const int t = b / (K / 8), r = b % (K / 8);
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (t < ntok) v = ld16(X + (row0 + t) * (size_t)K + kc + r * 8);
+    if (t < ntok) v = ld16(X + (row0 + t) * (size_t)K + r * 8);
     // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7)
-    const uint4 p = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
-    xs[b] = p;
-    float s = (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) + (bf16_lo(v.z) + bf16_hi(v.z)) +
-              (bf16_lo(v.w) + bf16_hi(v.w));
-    // the 8 blocks of one (token, group) are 8 consecutive threads
-    s = xsum_step<1>(s);
-    s = xsum_step<2>(s);
-    s = xsum_step<4>(s);
-    if ((r & 7) == 0) xsum[t * (PF_KC / 64) + (r >> 3)] = s;
+    xs[b ^ (t & 15)] = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                       __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
   }
 }
 
-// MODE 0: gate_up (pairs of rows j, I + j; writes bf16 silu(g) u)   MODE 1: down (writes f32)
-template <class F, int MODE>
+// per-lane weight data of 4 consecutive 64-input groups: raw fragments and (scale, min) pairs
+template <class F>
+struct Step {
+  typename Raw<F>::T raw[4];
+  uint32_t sc[4];
+};
+
+template <class F>
+DEV void load_step(const uint8_t* row, const void* ws, size_t n, int G0, int g, int K, Step<F>& s) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) F::load(row, G0 + i, g, s.raw[i]);
+  if (F::scale_group != 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.sc[i] = F::scale_raw(ws, n, G0 + i, K);
+  }
+}
+
+// MODE 0: gate_up (row pairs j, I + j; writes bf16 silu(g) u)   MODE 1: down (writes f32)
+//
+// Block = PF_WPB waves, wave w owns weight rows [r0, r0 + 16) (and the matching up rows).  A
+// block pass covers PF_TOK tokens of one expert: the token tile (all K inputs) is staged in LDS
+// once, then each wave streams its rows with weights and scales fetched one 4-group step
+// ahead of the matrix cores.  MFMA operands: A = tokens (lane: token l % 16), B = weights
+// (lane: row l % 16), so D[token 4 (l / 16) + i][row l % 16] sits in lane l: one weight row
+// per lane, one (scale, min) pair per group.  The group input sums X_g come from the same
+// MFMA against a fragment of bf16 ones.  Passes: blockIdx.z, then every gridDim.z-th.
+template <class F, int MODE, int K>
 __global__ void __launch_bounds__(PF_WPB * 64)
     k_grouped(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
-              const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N, int K,
+              const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
               size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int fixed_rows) {
-  __shared__ uint4 xs[PF_TOK * PF_KC / 8];
-  __shared__ float xsum[PF_TOK * (PF_KC / 64)];
-  // grouped: block x = expert; single matrix (fixed_rows >= 0): block x = 64-token pass
+  extern __shared__ uint4 xs[];  // PF_TOK rows of K / 8 blocks, block r of token t at r ^ t
   const int e = fixed_rows >= 0 ? 0 : blockIdx.x;
-  const int cnt = fixed_rows >= 0 ? min(PF_TOK, fixed_rows - (int)blockIdx.x * PF_TOK) : counts[e];
-  if (cnt <= 0) return;
-  const size_t off = fixed_rows >= 0 ? (size_t)blockIdx.x * PF_TOK : (size_t)offsets[e];
+  const int cnt = fixed_rows >= 0 ? fixed_rows : counts[e];
+  if ((int)blockIdx.z * PF_TOK >= cnt) return;
+  const size_t off = fixed_rows >= 0 ? 0 : (size_t)offsets[e];
   const int lane = lane_id(), wave = wave_id();
   const int g = lane >> 4, c16 = lane & 15;
-  const int tile = blockIdx.y * PF_WPB + wave;  // 16-row tile of output rows
-  const int rows_out = MODE == 0 ? N / 2 : N;   // gate_up: N = 2I weight rows, I outputs
-  const bool active = tile * 16 < rows_out;
-  const int r0 = tile * 16;
+  const int rows_out = MODE == 0 ? N / 2 : N;
+  const int r0 = (blockIdx.y * PF_WPB + wave) * 16;
+  const bool active = r0 < rows_out;
   const uint8_t* wq = Wq + (size_t)e * expert_q_bytes;
   const char* ws = reinterpret_cast<const char*>(Ws) + (size_t)e * expert_s_elems * s_elem_bytes;
   const size_t rb = F::row_bytes(K);
-  const uint8_t* rowA = wq + (size_t)(r0 + c16) * rb;                          // gate / down row
-  const uint8_t* rowB = wq + (size_t)((MODE == 0 ? N / 2 : 0) + r0 + c16) * rb;  // up row (gate_up)
-  for (int p0 = 0; p0 < cnt; p0 += PF_TOK) {
-    const int ntok = min(PF_TOK, cnt - p0);
-    const int ntiles = (ntok + 15) / 16;
-    f32x4 totA[4], totB[4], accA[4], accB[4];
+  const size_t nA = (size_t)(r0 + c16), nB = (size_t)((MODE == 0 ? N / 2 : 0) + r0 + c16);
+  const uint8_t* rowA = wq + nA * rb;
+  const uint8_t* rowB = wq + nB * rb;
+  constexpr int NG = K / 64;  // 64-input groups; weights run one 4-group step ahead
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  for (int pass = blockIdx.z; pass * PF_TOK < cnt; pass += gridDim.z) {
+    const int t0 = pass * PF_TOK;
+    const int ntok = min(PF_TOK, cnt - t0);
+    __syncthreads();
+    stage_tokens(X, off + t0, ntok, K, xs);
+    __syncthreads();
+    if (!active) continue;
+    f32x4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
+    const uint4* xrow = xs + (size_t)c16 * (K / 8);
+    auto compute = [&](const Step<F>& sa, const Step<F>& sbb, int G0) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) totA[t] = totB[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = 0; kc < K; kc += PF_KC) {
-      // weights of this chunk first, so their latency overlaps the token staging
-      typename Raw<F>::T rawA[PF_KC / 64], rawB[PF_KC / 64];
-      if (active) {
+      for (int i = 0; i < 4; ++i) {
+        const int G = G0 + i;
+        const uint4 x0 = xrow[(G * 8 + 2 * g) ^ c16], x1 = xrow[(G * 8 + 2 * g + 1) ^ c16];
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        uint4 a0, a1;
+        F::convert(sa.raw[i], a0, a1);
+        if (F::scale_group == 0) {
+          tA = mfma(x1, a1, mfma(x0, a0, tA));
+          if (MODE == 0) {
+            uint4 b0, b1;
+            F::convert(sbb.raw[i], b0, b1);
+            tB = mfma(x1, b1, mfma(x0, b0, tB));
+          }
+        } else {
+          const f32x4 accA = mfma(x1, a1, mfma(x0, a0, z));
+          f32x4 xg = z;
+          if (F::has_min) xg = mfma(x1, ones, mfma(x0, ones, z));
+          const float2 pa = F::scale_val(sa.sc[i]);
 #pragma unroll
-        for (int gi = 0; gi < PF_KC / 64; ++gi) {
-          F::load(rowA, kc / 64 + gi, g, rawA[gi]);
-          if (MODE == 0) F::load(rowB, kc / 64 + gi, g, rawB[gi]);
-        }
-      }
-      __syncthreads();
-      stage_tokens(X, off + p0, ntok, K, kc, xs, xsum);
-      __syncthreads();
-      if (!active) continue;
+          for (int r = 0; r < 4; ++r) tA[r] += F::has_min ? pa.x * accA[r] + (pa.y - 128.f * pa.x) * xg[r] : pa.x * accA[r];
+          if (MODE == 0) {
+            uint4 b0, b1;
+            F::convert(sbb.raw[i], b0, b1);
+            const f32x4 accB = mfma(x1, b1, mfma(x0, b0, z));
+            const float2 pb = F::scale_val(sbb.sc[i]);
 #pragma unroll
-      for (int gi = 0; gi < PF_KC / 64; ++gi) {
-        const int G = kc / 64 + gi;
-        uint4 a0, a1, b0, b1;
-        F::convert(rawA[gi], a0, a1);
-        if (MODE == 0) F::convert(rawB[gi], b0, b1);
-        // scales of the 4 output rows this lane holds in D: r0 + 4 g + i
-        float2 sA[4], sB[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sA[i] = F::scale(ws, (size_t)(r0 + 4 * g + i), G, K);
-          if (MODE == 0) sB[i] = F::scale(ws, (size_t)(N / 2 + r0 + 4 * g + i), G, K);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (t >= ntiles) break;
-          const int xrow = t * 16 + c16;
-          const uint4 x0 = xs[xrow * (PF_KC / 8) + gi * 8 + 2 * g];
-          const uint4 x1 = xs[xrow * (PF_KC / 8) + gi * 8 + 2 * g + 1];
-          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          if (F::scale_group == 64 || F::scale_group == 128) {
-            accA[t] = mfma(a1, x1, mfma(a0, x0, z));
-            if (MODE == 0) accB[t] = mfma(b1, x1, mfma(b0, x0, z));
-            const float X_g = F::has_min ? xsum[xrow * (PF_KC / 64) + gi] : 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              if (F::has_min) {
-                totA[t][i] += sA[i].x * accA[t][i] + (sA[i].y - 128.f * sA[i].x) * X_g;
-                if (MODE == 0) totB[t][i] += sB[i].x * accB[t][i] + (sB[i].y - 128.f * sB[i].x) * X_g;
-              } else {
-                totA[t][i] += sA[i].x * accA[t][i];
-                if (MODE == 0) totB[t][i] += sB[i].x * accB[t][i];
-              }
-            }
-          } else {  // one scale per row: accumulate raw sums, scale at the end
-            totA[t] = mfma(a1, x1, mfma(a0, x0, totA[t]));
-            if (MODE == 0) totB[t] = mfma(b1, x1, mfma(b0, x0, totB[t]));
+            for (int r = 0; r < 4; ++r)
+              tB[r] += F::has_min ? pb.x * accB[r] + (pb.y - 128.f * pb.x) * xg[r] : pb.x * accB[r];
           }
         }
       }
-    }
-    if (!active) continue;
-    float rsA[4] = {1.f, 1.f, 1.f, 1.f}, rsB[4] = {1.f, 1.f, 1.f, 1.f};
-    if (F::scale_group == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        rsA[i] = F::scale(ws, (size_t)(r0 + 4 * g + i), 0, K).x;
-        if (MODE == 0) rsB[i] = F::scale(ws, (size_t)(N / 2 + r0 + 4 * g + i), 0, K).x;
+    };
+    Step<F> s0, s1, s0b, s1b;
+    load_step<F>(rowA, ws, nA, 0, g, K, s0);
+    if (MODE == 0) load_step<F>(rowB, ws, nB, 0, g, K, s0b);
+    for (int G0 = 0; G0 < NG; G0 += 8) {
+      load_step<F>(rowA, ws, nA, G0 + 4, g, K, s1);
+      if (MODE == 0) load_step<F>(rowB, ws, nB, G0 + 4, g, K, s1b);
+      compute(s0, s0b, G0);
+      if (G0 + 8 < NG) {
+        load_step<F>(rowA, ws, nA, G0 + 8, g, K, s0);
+        if (MODE == 0) load_step<F>(rowB, ws, nB, G0 + 8, g, K, s0b);
       }
+      compute(s1, s1b, G0 + 4);
+    }
+    float rsA = 1.f, rsB = 1.f;
+    if (F::scale_group == 0) {
+      rsA = F::scale(ws, nA, 0, K).x;
+      if (MODE == 0) rsB = F::scale(ws, nB, 0, K).x;
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (t >= ntiles) break;
-      const int tok = p0 + t * 16 + c16;
-      if (tok >= cnt) continue;
+    for (int r = 0; r < 4; ++r) {
+      const int tok = 4 * g + r;
+      if (tok >= ntok) break;
+      const size_t slot = off + t0 + tok;
       if (MODE == 0) {
-        uint16_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gv = totA[t][i] * rsA[i], uv = totB[t][i] * rsB[i];
-          o[i] = to_bf16(silu(gv) * uv);
-        }
-        uint16_t* act = reinterpret_cast<uint16_t*>(out) + (off + tok) * (size_t)(N / 2) + r0 + 4 * g;
-        *reinterpret_cast<uint2*>(act) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+        reinterpret_cast<uint16_t*>(out)[slot * (size_t)(N / 2) + r0 + c16] = to_bf16(silu(tA[r] * rsA) * (tB[r] * rsB));
       } else {
-        float* y = reinterpret_cast<float*>(out) + (off + tok) * (size_t)N + r0 + 4 * g;
-        *reinterpret_cast<float4*>(y) =
-            make_float4(totA[t][0] * rsA[0], totA[t][1] * rsA[1], totA[t][2] * rsA[2], totA[t][3] * rsA[3]);
+        reinterpret_cast<float*>(out)[slot * (size_t)N + r0 + c16] = tA[r] * rsA;
       }
     }
   }
 }
 
-// grid x: experts (grouped) or 64-token passes (fixed_rows >= 0); grid y: 16-row tiles / PF_WPB
+// grid x: experts (grouped) or 1 (fixed_rows >= 0); y: 16-row tiles / PF_WPB; z: token passes
 template <class F>
 void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const int* offsets, const int* counts,
                     void* out, int E, int N, int K, int mode, size_t eq, size_t es, int sb, int fixed_rows,
                     hipStream_t st) {
   const int rows_out = mode == 0 ? N / 2 : N;
-  const int gx = fixed_rows >= 0 ? (fixed_rows + PF_TOK - 1) / PF_TOK : E;
-  const dim3 grid(gx, (rows_out / 16 + PF_WPB - 1) / PF_WPB);
+  const int passes = fixed_rows >= 0 ? (fixed_rows + PF_TOK - 1) / PF_TOK : PF_ZPASS;
+  const dim3 grid(fixed_rows >= 0 ? 1 : E, (rows_out / 16 + PF_WPB - 1) / PF_WPB, passes);
+  const size_t lds = (size_t)PF_TOK * K * 2;
   if (mode == 0)
-    hipLaunchKernelGGL((k_grouped<F, 0>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out, N, K, eq, es,
-                       sb, fixed_rows);
+    hipLaunchKernelGGL((k_grouped<F, 0, 2048>), grid, dim3(PF_WPB * 64), lds, st, wq, ws, X, offsets, counts, out, N,
+                       eq, es, sb, fixed_rows);
   else
-    hipLaunchKernelGGL((k_grouped<F, 1>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out, N, K, eq, es,
-                       sb, fixed_rows);
+    hipLaunchKernelGGL((k_grouped<F, 1, 512>), grid, dim3(PF_WPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq,
+                       es, sb, fixed_rows);
 }
 
 // gate_up then down for all experts of a grouped batch
@@ -298,7 +307,7 @@ int moe_prefill(const uint8_t* gu_q, const void* gu_s, const uint8_t* d_q, const
 template <class SH>
 int shared_prefill(const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s, const uint16_t* hn,
                    int rows, uint16_t* act, float* out, int H, int I, hipStream_t st) {
-  if (H % PF_KC != 0 || I % PF_KC != 0 || I % 16 != 0 || rows < 0) return -1;
+  if (H != 2048 || I != 512 || rows < 0) return -1;
   if (rows == 0) return 0;
   launch_grouped<FmtQ8<SH>>((const uint8_t*)sgu_q, sgu_s, hn, nullptr, nullptr, act, 1, 2 * I, H, 0, 0, 0, 2, rows, st);
   launch_grouped<FmtQ8<SH>>((const uint8_t*)sd_q, sd_s, act, nullptr, nullptr, out, 1, H, I, 1, 0, 0, 2, rows, st);

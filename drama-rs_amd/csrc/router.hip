@@ -231,7 +231,7 @@ __global__ void __launch_bounds__(64)
 
 // Canonical bf16 GEMM C = A . W^T (+ beta C).  Block = 4 waves; wave w holds MPW rows of A
 // (its lane chunks, as fp32) in registers and walks BN rows of W.  NCH = chunks per lane.
-constexpr int GM_MPW = 4, GM_BN = 32;
+constexpr int GM_MPW = 4, GM_BN = 4;
 
 template <int NCH>
 __global__ void __launch_bounds__(256)
@@ -256,6 +256,7 @@ __global__ void __launch_bounds__(256)
       a[r][8 * j + 6] = bf16_lo(v.w), a[r][8 * j + 7] = bf16_hi(v.w);
     }
   }
+#pragma unroll
   for (int nn = 0; nn < GM_BN; ++nn) {
     const int n = n0 + nn;
     if (n >= N) break;

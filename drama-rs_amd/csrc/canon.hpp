@@ -1,0 +1,203 @@
+// Canonical fp32 router arithmetic shared by the router kernels and the fused decode step
+// (reference semantics: kernels/drama.cu:178-200,317-461).
+//
+// Every function fixes its operation order, so the CPU oracle reproduces logits, softmax
+// probabilities and therefore the selected experts bit for bit:
+//   RMSNorm  lane l accumulates x^2 over float4 indices l + 64 j with fmaf, 64-lane xor
+//            butterfly, t = ss * (1 / K) + eps, inv = canon_rsqrt(t), xn = (x * inv) * nw
+//   dot      lane l owns 8-element chunks l + 64 j, fmaf in element order, xor butterfly
+//   top-k    k rounds of (logit desc, index asc), NaN logits last (the logit order is the
+//            probability order; selecting on logits needs no exp or division per expert)
+//   softmax  m = max logit, ex = exp(l - m) with canon_exp, lane l sums experts l + 64 j in
+//            order, xor butterfly = z; p_k = ex_k / z (correctly rounded) for the picks;
+//            total = sum of picked p in pick order; wts = p / total
+// No expression in here may be contracted into an fma: every body switches contraction off
+// and no header math helper is used.
+#pragma once
+#include "common.hpp"
+
+namespace drm {
+
+// exp: Cody-Waite reduction with k = rint(x log2 e), ln 2 split in a 16-bit head and a tail,
+// degree-8 Taylor polynomial of e^r in Horner form with fma, scaling by 2^k through the
+// exponent field.  Inputs below -86.5 give 0 and above 88 give +inf, so no subnormal result
+// is ever formed.  Accuracy: within 2 ulp of exp on the range that matters (x <= 0).
+DEV float canon_exp(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  if (x < -86.5f) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  const float k = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(-k, 0.693145751953125f, x);
+  r = __builtin_fmaf(-k, 1.428606765330187e-06f, r);
+  float p = 2.48015873e-05f;
+  p = __builtin_fmaf(p, r, 1.98412698e-04f);
+  p = __builtin_fmaf(p, r, 1.38888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ki = (int)k;
+  return p * __uint_as_float((uint32_t)(ki + 127) << 23);
+}
+
+// 1 / sqrt(t) for t > 0 from plain multiplies and subtractions only, so every step rounds
+// the same way on any IEEE machine: seed from the exponent/mantissa bit pattern
+// (0x5f3759df - bits / 2), then three Newton steps y = y * (1.5 - (0.5 t) * (y * y)).
+// Relative error <= 2e-7.
+DEV float canon_rsqrt(float t) {
+#pragma clang fp contract(off)
+  float y = __uint_as_float(0x5f3759dfu - (__float_as_uint(t) >> 1));
+  const float h = 0.5f * t;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float yy = y * y;
+    const float hyy = h * yy;
+    const float c = 1.5f - hyy;
+    y = y * c;
+  }
+  return y;
+}
+
+// Canonical RMSNorm scale from the lane's float4 values xr[j] = x4[lane + 64 j], j < NRM
+// (K = 256 NRM); every lane gets the same bits.
+template <int NRM>
+DEV float canon_rms_inv_regs(const float4 (&xr)[NRM], float eps) {
+#pragma clang fp contract(off)
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NRM; ++j) {
+    ss = __builtin_fmaf(xr[j].x, xr[j].x, ss);
+    ss = __builtin_fmaf(xr[j].y, xr[j].y, ss);
+    ss = __builtin_fmaf(xr[j].z, xr[j].z, ss);
+    ss = __builtin_fmaf(xr[j].w, xr[j].w, ss);
+  }
+  ss = wave_sum(ss);
+  const float t = ss * (1.0f / (float)(NRM * 256)) + eps;
+  return canon_rsqrt(t);
+}
+
+// xn = (x * inv) * nw, element by element
+DEV float4 canon_norm4(float4 a, float inv, float4 n) {
+#pragma clang fp contract(off)
+  return make_float4((a.x * inv) * n.x, (a.y * inv) * n.y, (a.z * inv) * n.z, (a.w * inv) * n.w);
+}
+
+// One logit row: w[j] = the row's bf16 chunk lane + 64 j, (a[j], b[j]) = the matching 8
+// normalised inputs.  Returns the wave total (same bits on every lane).
+template <int NCH>
+DEV float canon_row_dot(const uint4 (&w)[NCH], const float4 (&a)[NCH], const float4 (&b)[NCH]) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    acc = __builtin_fmaf(bf16_lo(w[j].x), a[j].x, acc);
+    acc = __builtin_fmaf(bf16_hi(w[j].x), a[j].y, acc);
+    acc = __builtin_fmaf(bf16_lo(w[j].y), a[j].z, acc);
+    acc = __builtin_fmaf(bf16_hi(w[j].y), a[j].w, acc);
+    acc = __builtin_fmaf(bf16_lo(w[j].z), b[j].x, acc);
+    acc = __builtin_fmaf(bf16_hi(w[j].z), b[j].y, acc);
+    acc = __builtin_fmaf(bf16_lo(w[j].w), b[j].z, acc);
+    acc = __builtin_fmaf(bf16_hi(w[j].w), b[j].w, acc);
+  }
+  return wave_sum(acc);
+}
+
+// Top-k selection key of a logit: an int whose order is the float order of the logit
+// (negative values have their magnitude bits flipped, so -0 sorts just below +0); a NaN
+// logit gets KEY_NAN, below every number; picked experts KEY_PICKED, padding KEY_PAD.
+constexpr int KEY_PAD = -2147483647 - 1, KEY_PICKED = KEY_PAD + 1, KEY_NAN = KEY_PAD + 2;
+DEV int canon_logit_key(float v) {
+  const int i = __float_as_int(v);
+  return v != v ? KEY_NAN : (i >= 0 ? i : i ^ 0x7fffffff);
+}
+
+template <int O>
+DEV int xmax_step_i(int v) {
+  float a, b;
+  xchg<O>(__int_as_float(v), a, b);
+  return max(__float_as_int(a), __float_as_int(b));
+}
+DEV int wave_max_i(int v) {
+  v = xmax_step_i<1>(v);
+  v = xmax_step_i<2>(v);
+  v = xmax_step_i<4>(v);
+  v = xmax_step_i<8>(v);
+  v = xmax_step_i<16>(v);
+  return xmax_step_i<32>(v);
+}
+
+// Top-k selection over E <= 256 logits by one wave: k rounds of (logit desc, index asc)
+// on canon_logit_key.  Lane k < topk receives the expert of pick k.  Expert e = lane + 64 j
+// lives in lane e % 64, slot j = e / 64, so among equal keys the lowest index is the first
+// lane of the first slot whose ballot is non-empty.  Every pick is a distinct expert below E.
+DEV int canon_select_topk(const float* __restrict__ l, int E, int topk) {
+  const int lane = lane_id();
+  int key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + WAVE * j;
+    key[j] = e < E ? canon_logit_key(l[e]) : KEY_PAD;
+  }
+  int id = 0;
+  for (int k = 0; k < topk; ++k) {
+    const int kb = wave_max_i(max(max(key[0], key[1]), max(key[2], key[3])));
+    const uint64_t b0 = __ballot(key[0] == kb), b1 = __ballot(key[1] == kb), b2 = __ballot(key[2] == kb),
+                   b3 = __ballot(key[3] == kb);
+    const int js = b0 ? 0 : b1 ? 1 : b2 ? 2 : 3;
+    const uint64_t bj = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
+    const int ls = (int)__builtin_ctzll(bj);
+    if (lane == ls) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j == js) key[j] = KEY_PICKED;
+    }
+    if (lane == k) id = ls + WAVE * js;
+  }
+  return id;
+}
+
+// Softmax denominator: m = max of the non-NaN logits, z = sum of canon_exp(l - m) with lane
+// l summing experts l + 64 j in order, then the xor butterfly.  Same bits on every lane.
+DEV float canon_softmax_z(const float* __restrict__ l, int E, float* m_out) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + WAVE * j;
+    v[j] = e < E ? l[e] : -__builtin_inff();
+  }
+  const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+  float z = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + WAVE * j;
+    z = z + (e < E ? canon_exp(v[j] - m) : 0.f);
+  }
+  *m_out = m;
+  return wave_sum(z);
+}
+
+// Renormalised weight of the pick held by this lane (lane k < topk holds pick k, logit lk):
+// p_k = canon_exp(lk - m) / z, total = sum of p_k in pick order, w_k = p_k / total.
+DEV float canon_topk_weight(float lk, float m, float z, int topk) {
+#pragma clang fp contract(off)
+  const float p = canon_exp(lk - m) / z;
+  float total = 0.f;
+  for (int k = 0; k < topk; ++k) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), k));
+  return p / total;
+}
+
+// Softmax + top-k of one row by one wave; lane k < topk receives pick k and its weight.
+DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* my_idx, float* my_w) {
+  const int id = canon_select_topk(l, E, topk);
+  float m;
+  const float z = canon_softmax_z(l, E, &m);
+  *my_idx = id;
+  *my_w = canon_topk_weight(l[lane_id() < topk ? id : 0], m, z, topk);
+}
+
+}  // namespace drm

@@ -1,128 +1,16 @@
 // Router: logits, softmax and top-k (reference: kernels/drama.cu:317-468, src/ffi.rs:41,55-59)
 // plus the bf16 GEMM dr_gemm that the prefill router uses (src/engine.rs:554).
 //
-// These kernels follow one canonical fp32 operation order, so the CPU oracle reproduces the
-// logits, the softmax probabilities and hence the selected experts bit for bit:
-//   RMSNorm  lane l accumulates x^2 over float4 indices l + 64 j with fmaf, 64-lane xor
-//            butterfly, t = ss * (1 / K) + eps, inv = canon_rsqrt(t), xn = (x * inv) * nw
-//   dot      lane l owns 8-element chunks l + 64 j, fmaf in element order, xor butterfly
-//   softmax  ex = exp(l - max) with the library's own exp (below), lane l sums experts
-//            l + 64 j in order, xor butterfly, p = ex / z (correctly rounded)
-//   top-k    k rounds of (p desc, index asc); total = sum of picked p in pick order;
-//            wts = p / total
-#include "common.hpp"
+// These kernels follow the canonical fp32 operation order of canon.hpp (RMSNorm, row dot,
+// softmax, top-k), so the CPU oracle reproduces the logits, the softmax probabilities and
+// hence the selected experts bit for bit.
+#include "canon.hpp"
 
 #pragma clang fp contract(off)
 
 using namespace drm;
 
 namespace {
-
-// exp: Cody-Waite reduction with k = rint(x log2 e), ln 2 split in a 16-bit head and a tail,
-// degree-8 Taylor polynomial of e^r in Horner form with fma, scaling by 2^k through the
-// exponent field.  Inputs below -86.5 give 0 and above 88 give +inf, so no subnormal result
-// is ever formed.  Accuracy: within 2 ulp of exp on the range that matters (x <= 0).
-DEV float canon_exp(float x) {
-  if (x != x) return x;
-  if (x < -86.5f) return 0.0f;
-  if (x > 88.0f) return __builtin_inff();
-  const float k = __builtin_rintf(x * 1.44269504088896341f);
-  float r = __builtin_fmaf(-k, 0.693145751953125f, x);
-  r = __builtin_fmaf(-k, 1.428606765330187e-06f, r);
-  float p = 2.48015873e-05f;
-  p = __builtin_fmaf(p, r, 1.98412698e-04f);
-  p = __builtin_fmaf(p, r, 1.38888889e-03f);
-  p = __builtin_fmaf(p, r, 8.33333333e-03f);
-  p = __builtin_fmaf(p, r, 4.16666667e-02f);
-  p = __builtin_fmaf(p, r, 1.66666667e-01f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  const int ki = (int)k;
-  return p * __uint_as_float((uint32_t)(ki + 127) << 23);
-}
-
-// 1 / sqrt(t) for t > 0 from plain multiplies and subtractions only, so every step rounds
-// the same way on any IEEE machine: seed from the exponent/mantissa bit pattern
-// (0x5f3759df - bits / 2), then three Newton steps y = y * (1.5 - (0.5 t) * (y * y)).
-// Relative error <= 2e-7.  Nothing here may be contracted into an fma (this file is compiled
-// with contraction off and uses no header math helpers).
-DEV float canon_rsqrt(float t) {
-  float y = __uint_as_float(0x5f3759dfu - (__float_as_uint(t) >> 1));
-  const float h = 0.5f * t;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const float yy = y * y;
-    const float hyy = h * yy;
-    const float c = 1.5f - hyy;
-    y = y * c;
-  }
-  return y;
-}
-
-// Canonical 1 / sqrt(mean(x^2) + eps) of a K-float vector; every lane of the wave gets it.
-template <int K>
-DEV float canon_rms_inv(const float* __restrict__ x, float eps) {
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  float ss = 0.f;
-#pragma unroll
-  for (int c = lane_id(); c < K / 4; c += WAVE) {
-    const float4 v = x4[c];
-    ss = __builtin_fmaf(v.x, v.x, ss);
-    ss = __builtin_fmaf(v.y, v.y, ss);
-    ss = __builtin_fmaf(v.z, v.z, ss);
-    ss = __builtin_fmaf(v.w, v.w, ss);
-  }
-  ss = wave_sum(ss);
-  const float t = ss * (1.0f / (float)K) + eps;
-  return canon_rsqrt(t);
-}
-
-// Softmax + top-k of one row of logits by one wave; lane k < topk receives pick k.
-DEV void canon_softmax_topk(const float* __restrict__ l, int E, int topk, int* my_idx, float* my_w) {
-  const int lane = lane_id();
-  float v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + WAVE * j;
-    v[j] = e < E ? l[e] : -__builtin_inff();
-  }
-  const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-  float ex[4], z = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + WAVE * j;
-    ex[j] = e < E ? canon_exp(v[j] - m) : 0.f;
-    z = z + ex[j];
-  }
-  z = wave_sum(z);
-  // Selection keys: p for valid experts, -1 for a NaN probability, -2 once picked, -3 for
-  // padding slots e >= E; the running best starts at -4.  Every round therefore picks a
-  // distinct expert below E (topk <= E), whatever the logits hold.
-  float p[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float q = ex[j] / z;
-    p[j] = (lane + WAVE * j) < E ? (q != q ? -1.f : q) : -3.f;
-  }
-  float total = 0.f, w = 0.f;
-  int id = 0;
-  for (int k = 0; k < topk; ++k) {
-    float bv = -4.f;
-    int bi = 1 << 30;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (p[j] > bv) bv = p[j], bi = lane + WAVE * j;
-    wave_argmax(bv, bi);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lane + WAVE * j == bi) p[j] = -2.f;
-    total = total + bv;
-    if (lane == k) w = bv, id = bi;
-  }
-  *my_idx = id;
-  *my_w = w / total;
-}
 
 constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
 
@@ -164,36 +52,11 @@ __global__ void __launch_bounds__(RT_WPB * 64)
       }
 #pragma unroll
       for (int j = 0; j < NRM; ++j) xr[j] = x4[lane + WAVE * j];
-      float ss = 0.f;
+      inv = canon_rms_inv_regs<NRM>(xr, eps);
 #pragma unroll
-      for (int j = 0; j < NRM; ++j) {
-        ss = __builtin_fmaf(xr[j].x, xr[j].x, ss);
-        ss = __builtin_fmaf(xr[j].y, xr[j].y, ss);
-        ss = __builtin_fmaf(xr[j].z, xr[j].z, ss);
-        ss = __builtin_fmaf(xr[j].w, xr[j].w, ss);
-      }
-      ss = wave_sum(ss);
-      const float t = ss * (1.0f / (float)K) + eps;
-      inv = canon_rsqrt(t);
+      for (int j = 0; j < NCH; ++j) xa[j] = canon_norm4(xa[j], inv, na[j]), xb[j] = canon_norm4(xb[j], inv, nb[j]);
     }
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      float4 a = xa[j], b = xb[j];
-      if (nw) {
-        a = make_float4((a.x * inv) * na[j].x, (a.y * inv) * na[j].y, (a.z * inv) * na[j].z, (a.w * inv) * na[j].w);
-        b = make_float4((b.x * inv) * nb[j].x, (b.y * inv) * nb[j].y, (b.z * inv) * nb[j].z, (b.w * inv) * nb[j].w);
-      }
-      acc = __builtin_fmaf(bf16_lo(w[j].x), a.x, acc);
-      acc = __builtin_fmaf(bf16_hi(w[j].x), a.y, acc);
-      acc = __builtin_fmaf(bf16_lo(w[j].y), a.z, acc);
-      acc = __builtin_fmaf(bf16_hi(w[j].y), a.w, acc);
-      acc = __builtin_fmaf(bf16_lo(w[j].z), b.x, acc);
-      acc = __builtin_fmaf(bf16_hi(w[j].z), b.y, acc);
-      acc = __builtin_fmaf(bf16_lo(w[j].w), b.z, acc);
-      acc = __builtin_fmaf(bf16_hi(w[j].w), b.w, acc);
-    }
-    acc = wave_sum(acc);
+    const float acc = canon_row_dot<NCH>(w, xa, xb);
     if (lane == 0) __hip_atomic_store(logits + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(0);

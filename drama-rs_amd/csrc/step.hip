@@ -1,0 +1,478 @@
+// Fused batch-1 decode step: router, top-k, int4 gate_up + SiLU*up, down + weighted combine
+// and the int8 shared expert of n_layers MoE layers in ONE persistent launch.  It computes
+// exactly what the engine's per-layer chain dr_router_topk -> dr_moe_decode computes
+// (reference: src/engine.rs:1001-1007 recording kernels/drama.cu:369-461,470-599 per layer),
+// with routing bit-exact to the canonical router order of canon.hpp.
+//
+// Why one launch: a layer streams ~18 MB, 2.3 us at the HBM roofline, while each dependent
+// launch costs ~1.5 us on MI355X before its first load issues.  Here 256 workgroups (one per
+// CU, 8 waves each) stay resident for the whole step and hand data to each other through
+// three all-to-all exchanges per layer: the 257 router logits, the 9 x 512 activations and
+// the 2048-float residual stream.  Each exchange is a "low latency" slot array: every value
+// travels in a 64-bit word with a tag (fp32 bits + 32-bit tag; the routed activations two
+// 24-bit floats + 16-bit tag, which halves the largest exchange), written with one cache-bypassing
+// (device-scope) store and read with device-scope loads until every word carries the tag of
+// the current phase.  A 64-bit access is single-copy atomic, so a reader never sees a value
+// without its tag and no separate flag, fence or counter is needed: one memory hop per
+// exchange.  Tags are epoch * 4096 + 3 layer + phase + 1, with the epoch read from sync[0] at
+// launch and advanced by the launch's last act, so slots never need clearing between calls.
+//
+// Work map (g = global wave, 0..2047): router row g/8 on wave 0 of every block (row 256, the
+// shared-expert gate, on block 0 wave 1); routed gate_up pairs j, j+1 of expert slot g/256
+// with j = 2g mod 512; shared gate_up pair g/4 on waves 2 and 6; down output row g.  Every
+// wave polls one eighth of each exchange.  A wave's loads return in order, so weight loads
+// are placed where no poll has to wait for them: the routed gate_up and down rows right
+// after top-k (needed next anyway), the next layer's router and shared gate_up rows right
+// after the activation poll, so they stream in during the down phase and the exchanges.
+//
+// Every wait is bounded: after ~0.2 s without progress the block writes sync[1] = 1 and
+// returns, and a launch that finds sync[1] != 0 returns at once, so the grid always drains.
+#include "canon.hpp"
+#include "drama_moe.h"
+
+using namespace drm;
+
+namespace {
+
+constexpr int ST_H = 2048, ST_I = 512, ST_TOPK = 8, ST_MAXE = 256;
+constexpr int ST_NB = 256, ST_WPB = 8, ST_NT = ST_WPB * 64, ST_NP = 8;  // every wave polls a share
+constexpr uint32_t ST_TAG_STRIDE = 4096;
+constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
+constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
+
+// slot arrays (64-bit words) inside the caller's ll buffer
+constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + (ST_TOPK + 1) * ST_I, LL_WORDS = LL_X + ST_H;
+static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
+
+// Phase timestamps for development builds (-DST_TRACE): thread 0 of each block stores the
+// 100 MHz clock at points 0..7 and 11..14 of each layer (poll rounds at 8..10, 15) into
+// words LL_WORDS.. of a larger ll buffer.
+#ifdef ST_TRACE
+#define ST_PUT(pt, v) \
+  if (threadIdx.x == 0) ll[LL_WORDS + ((size_t)l * 16 + (pt)) * ST_NB + blockIdx.x] = (v)
+#define ST_MARK(pt) ST_PUT(pt, __builtin_amdgcn_s_memrealtime())
+#define ST_MARKW(pt, w) \
+  if (threadIdx.x == 64 * (w)) ll[LL_WORDS + ((size_t)l * 16 + (pt)) * ST_NB + blockIdx.x] = __builtin_amdgcn_s_memrealtime()
+#else
+#define ST_MARKW(pt, w)
+#define ST_PUT(pt, v)
+#define ST_MARK(pt)
+#endif
+
+DEV void ll_put(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DEV uint64_t ll_get(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Two activations in one word: tag (16 bits) and both values rounded to nearest-even
+// 24-bit floats (sign, exponent, 15 mantissa bits; relative error <= 2^-16).  The 16-bit
+// tag still tells the current phase from the slot's previous content: that always carries
+// the previous layer's tag (3 less) or the previous launch's (a different epoch).
+DEV uint32_t f24(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+}
+DEV void ll_put2(uint64_t* p, float a, float b, uint32_t tag) {
+  const uint64_t w = ((uint64_t)(tag & 0xffffu) << 48) | ((uint64_t)f24(a) << 24) | (uint64_t)f24(b);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DEV float2 ll_val2(uint64_t w) {
+  return make_float2(__uint_as_float((uint32_t)(w >> 16) & 0xffffff00u), __uint_as_float((uint32_t)(w << 8)));
+}
+
+// LDS float4 slots: int4 rows give lane l the 32 inputs [32 l, 32 l + 32) -> slot i * 64 + l
+DEV int slot_q4(int f) { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
+// int8 K = 2048 rows give lane l bytes [16 l, +16) and [1024 + 16 l, +16)
+DEV int slot_q8(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
+
+// Wave share of an exchange: wave p of NP owns, in lane l, the words base[l + 64 r] of rows
+// r = p + NP i, i < N.  It reloads the words whose tag is not yet the phase's until all are
+// current, then hands each to spec.store.  Returns the rounds taken, 0 after ~0.2 s (the
+// caller aborts).
+template <int N, int NP, class Spec>
+DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync) {
+  const int lane = lane_id();
+  const uint64_t* b = base + lane + 64 * p;
+  uint64_t v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int r = p + NP * i;
+    v[i] = sp.valid(r, lane + 64 * r) ? ll_get(b + 64 * NP * i) : sp.ready(r);
+  }
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t it = 1;
+  for (;; ++it) {
+    bool good = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) good &= sp.ok(p + NP * i, v[i]);
+    if (__ballot(!good) == 0) break;
+    if ((it & 63) == 0 && __builtin_amdgcn_s_memrealtime() - t0 > ST_TIMEOUT_TICKS) {
+      if (lane == 0) __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return 0;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (!sp.ok(p + NP * i, v[i])) v[i] = ll_get(b + 64 * NP * i);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int r = p + NP * i;
+    if (sp.valid(r, lane + 64 * r)) sp.store(r, lane + 64 * r, v[i]);
+  }
+  return it;
+}
+
+// one fp32 value per word: logits (words 0..E) and the residual stream (2048 words)
+struct Spec32 {
+  uint32_t tag;
+  int n;
+  float* dst;
+  DEV bool valid(int, int w) const { return w < n; }
+  DEV uint64_t ready(int) const { return (uint64_t)tag << 32; }
+  DEV bool ok(int, uint64_t v) const { return (uint32_t)(v >> 32) == tag; }
+  DEV void store(int, int w, uint64_t v) const { dst[w] = __uint_as_float((uint32_t)v); }
+};
+
+// activations: words 0..2047 hold routed elements 2w, 2w + 1 (packed, i < 32), words
+// 2048..2559 shared element w - 2048 (one per word, i >= 32); stored into the down slots
+struct SpecAct {
+  uint32_t tag;
+  float* dst;  // as4 as floats
+  DEV bool valid(int r, int) const { return r < 40; }
+  DEV uint64_t ready(int i) const { return i < 32 ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32; }
+  DEV bool ok(int i, uint64_t v) const {
+    return i < 32 ? (v >> 48) == (tag & 0xffffu) : (uint32_t)(v >> 32) == tag;
+  }
+  DEV void store(int i, int w, uint64_t v) const {
+    if (i < 32) {
+      const float2 p = ll_val2(v);
+      float* d = dst + slot_q4(w >> 1) * 4 + (w & 1) * 2;
+      d[0] = p.x, d[1] = p.y;
+    } else {
+      const int e = w - 2048;
+      dst[(1024 + ((e >> 2) & 1) * 64 + (e >> 3)) * 4 + (e & 3)] = __uint_as_float((uint32_t)v);
+    }
+  }
+};
+
+struct RouterRow {
+  uint4 w[4];
+};
+struct SharedPair {
+  uint4 g0, g1, u0, u1;
+  float sg0, sg1, su0, su1;
+};
+
+template <class SH>
+DEV void load_shared_pair(const dr_decode_layer& Ly, int j, int lane, SharedPair& s) {
+  constexpr int H = ST_H, I = ST_I;
+  const int8_t* rg = Ly.sgu_q + (size_t)j * H + lane * 16;
+  const int8_t* ru = Ly.sgu_q + (size_t)(I + j) * H + lane * 16;
+  s.g0 = ld16(rg), s.g1 = ld16(rg + 1024), s.u0 = ld16(ru), s.u1 = ld16(ru + 1024);
+  s.sg0 = SH::scale(Ly.sgu_s, j, lane * 16, H), s.sg1 = SH::scale(Ly.sgu_s, j, 1024 + lane * 16, H);
+  s.su0 = SH::scale(Ly.sgu_s, I + j, lane * 16, H), s.su1 = SH::scale(Ly.sgu_s, I + j, 1024 + lane * 16, H);
+}
+
+template <class SC, class SH>
+__global__ void __launch_bounds__(ST_NT, 1)
+    k_decode_step(const dr_decode_layer* __restrict__ layers, int L, float* x, int E, float eps,
+                  uint64_t* __restrict__ ll, uint32_t* __restrict__ sync, int* __restrict__ idx_out,
+                  float* __restrict__ wts_out, float* __restrict__ sgate_out, float* __restrict__ xs_out) {
+  constexpr int H = ST_H, I = ST_I;
+  __shared__ float4 xr4[H / 4];                        // residual stream x (raw)
+  __shared__ float4 nws[H / 4];                        // RMSNorm weight of the layer
+  __shared__ float4 xq4[H / 4], xq8[H / 4];            // normalised x in the int4 / int8 lane slots
+  __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
+  __shared__ float lg[ST_MAXE + 1];
+  __shared__ int s_sel[ST_TOPK];
+  __shared__ float s_mz[2];
+  __shared__ int s_abort;
+  if (__syncthreads_or(__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) return;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int pw = wave;  // every wave polls rows pw + 8 i of each exchange
+  const bool poller = true;
+  const int g = blockIdx.x * ST_WPB + wave;
+  const uint32_t epoch = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t tag0 = epoch * ST_TAG_STRIDE + 1;
+
+  const bool is_router = (wave == 0 && (int)blockIdx.x <= E) || (wave == 1 && blockIdx.x == 0 && E == ST_MAXE);
+  const int rrow = wave == 0 ? (int)blockIdx.x : ST_MAXE;
+  const bool is_shared = (wave & 3) == 2;
+  const int sj = g >> 2;               // shared gate_up pair
+  const int rk = g >> 8;               // routed expert slot of the gate_up pairs
+  const int rj = (2 * g) & (I - 1);    // first of the two gate_up pairs
+  const int ka = lane >> 4, cc = lane & 15;  // down: lane's expert slots ka, 4 + ka and chunk
+  const int n = g;                     // down output row
+
+  RouterRow rw;
+  SharedPair sp;
+  float4 nwv = make_float4(1.f, 1.f, 1.f, 1.f);
+  if (tid == 0) s_abort = 0;
+  {
+    const dr_decode_layer L0 = layers[0];
+    if (is_router) {
+      const uint16_t* wr = L0.router + (size_t)rrow * H;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
+    }
+    if (is_shared) load_shared_pair<SH>(L0, sj, lane, sp);
+    if (L0.nw) nwv = reinterpret_cast<const float4*>(L0.nw)[tid];
+    nws[tid] = nwv;
+    xr4[tid] = reinterpret_cast<const float4*>(x)[tid];
+  }
+  __syncthreads();
+
+  for (int l = 0; l < L; ++l) {
+    const dr_decode_layer Ly = layers[l];
+    const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2;
+    ST_MARK(0);
+    float res;  // x[n], read now: the poller overwrites xr4 during the down phase
+
+    // ---- RMSNorm (canonical, every wave) and the router row; the poller collects logits
+    {
+      res = reinterpret_cast<const float*>(xr4)[n];
+      float4 xr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xr[j] = xr4[lane + 64 * j];
+      const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
+      {
+        const float4 xn = canon_norm4(xr4[tid], inv, nwv);
+        xq4[slot_q4(tid)] = xn;
+        xq8[slot_q8(tid)] = xn;
+      }
+      if (is_router) {
+        float4 a[4], b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + 64 * j;
+          a[j] = canon_norm4(xr4[2 * c], inv, nws[2 * c]);
+          b[j] = canon_norm4(xr4[2 * c + 1], inv, nws[2 * c + 1]);
+        }
+        const float acc = canon_row_dot<4>(rw.w, a, b);
+        if (lane == 0) ll_put(ll + LL_LOG + rrow, acc, tA);
+      }
+      ST_MARK(1);
+    }
+    if (poller) {
+      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync);
+      if (!r && lane == 0) s_abort = 1;
+      ST_PUT(8, r);
+    }
+    __syncthreads();
+    ST_MARK(2);
+    if (s_abort) return;
+
+    // ---- top-k: selection on wave 0 and the softmax denominator on wave 1, side by side
+    if (wave == 0) {
+      const int id = canon_select_topk(lg, E, ST_TOPK);
+      if (lane < ST_TOPK) s_sel[lane] = id;
+    } else if (wave == 1) {
+      float m;
+      const float z = canon_softmax_z(lg, E, &m);
+      if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+    }
+    __syncthreads();
+
+    {
+      const int my_idx = s_sel[lane & (ST_TOPK - 1)];
+      const float my_w = canon_topk_weight(lg[my_idx], s_mz[0], s_mz[1], ST_TOPK);
+      const float sgv = sigmoid(lg[E]);
+      ST_MARK(3);
+      if (blockIdx.x == 0 && wave == 0) {
+        if (idx_out && lane < ST_TOPK) idx_out[l * ST_TOPK + lane] = my_idx;
+        if (wts_out && lane < ST_TOPK) wts_out[l * ST_TOPK + lane] = my_w;
+        if (sgate_out && lane == 0) sgate_out[l] = lg[E];
+      }
+
+      // ---- routed weight loads: gate_up pairs, then the down row (8 experts + shared)
+      const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
+      const uint8_t* q = Ly.gu_q + ek * (2 * I) * (H / 2) + lane * 16;
+      const uint32_t* sm = reinterpret_cast<const uint32_t*>(Ly.gu_s) + ek * (2 * I) * (H / 64) + (lane >> 1);
+      uint4 wg[2], wu[2];
+      uint32_t sg[2], su[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int j = rj + p;
+        wg[p] = ld16(q + (size_t)j * (H / 2));
+        wu[p] = ld16(q + (size_t)(I + j) * (H / 2));
+        sg[p] = sm[(size_t)j * (H / 64)];
+        su[p] = sm[(size_t)(I + j) * (H / 64)];
+      }
+      const size_t ea = (size_t)__shfl(my_idx, ka), eb = (size_t)__shfl(my_idx, 4 + ka);
+      const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
+      const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
+      const uint4 qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
+      const uint4 qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
+      const uint32_t da_s = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
+      const uint32_t db_s = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
+      const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
+      const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
+
+      // ---- gate_up: two routed pairs per wave, one shared pair on waves 2 and 6
+      {
+        float xv[32], xsum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float4 v = xq4[i * 64 + lane];
+          xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
+          xsum += (v.x + v.y) + (v.z + v.w);
+        }
+        float av[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          float qg = 0.f, qu = 0.f;
+          qg = dot8_q4(wg[p].x, xv + 0, qg), qu = dot8_q4(wu[p].x, xv + 0, qu);
+          qg = dot8_q4(wg[p].y, xv + 8, qg), qu = dot8_q4(wu[p].y, xv + 8, qu);
+          qg = dot8_q4(wg[p].z, xv + 16, qg), qu = dot8_q4(wu[p].z, xv + 16, qu);
+          qg = dot8_q4(wg[p].w, xv + 24, qg), qu = dot8_q4(wu[p].w, xv + 24, qu);
+          const float2 a = SC::pair(sg[p]), b = SC::pair(su[p]);
+          const float gv = wave_sum(a.x * qg + a.y * xsum);
+          const float uv = wave_sum(b.x * qu + b.y * xsum);
+          av[p] = silu(gv) * uv;
+        }
+        if (lane == 0) ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
+      }
+      if (is_shared) {
+        float xa[16], xb[16], sa = 0.f, sb = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 v = xq8[i * 64 + lane], w = xq8[256 + i * 64 + lane];
+          xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+          xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+          sa += (v.x + v.y) + (v.z + v.w);
+          sb += (w.x + w.y) + (w.z + w.w);
+        }
+        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
+        const uint32_t gw0[4] = {sp.g0.x, sp.g0.y, sp.g0.z, sp.g0.w}, gw1[4] = {sp.g1.x, sp.g1.y, sp.g1.z, sp.g1.w};
+        const uint32_t uw0[4] = {sp.u0.x, sp.u0.y, sp.u0.z, sp.u0.w}, uw1[4] = {sp.u1.x, sp.u1.y, sp.u1.z, sp.u1.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          ga = dot4_u8b(gw0[d], xa + 4 * d, ga), gb = dot4_u8b(gw1[d], xb + 4 * d, gb);
+          ua = dot4_u8b(uw0[d], xa + 4 * d, ua), ub = dot4_u8b(uw1[d], xb + 4 * d, ub);
+        }
+        const float gv = wave_sum(sp.sg0 * (ga - 128.f * sa) + sp.sg1 * (gb - 128.f * sb));
+        const float uv = wave_sum(sp.su0 * (ua - 128.f * sa) + sp.su1 * (ub - 128.f * sb));
+        if (lane == 0) ll_put(ll + LL_ACT + ST_TOPK * I / 2 + sj, silu(gv) * uv, tB);
+      }
+      ST_MARK(4);
+
+      // ---- activation exchange, collected by the poller
+      ST_MARKW(14, 2);
+      if (poller) {
+        ST_MARKW(12, 7);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4)}, sync);
+        if (!r && lane == 0) s_abort = 1;
+        ST_MARKW(13, 7);
+#ifdef ST_TRACE
+        if (threadIdx.x == 448) ll[LL_WORDS + ((size_t)l * 16 + 15) * ST_NB + blockIdx.x] = r;
+#endif
+      }
+      __syncthreads();
+      ST_MARK(5);
+      if (s_abort) return;
+
+      // ---- next layer's known weights: issued after the activation poll (a wave's loads
+      // return in order, so loads issued before a poll would delay it)
+      if (l + 1 < L) {
+        const dr_decode_layer Ln = layers[l + 1];
+        if (is_router) {
+          const uint16_t* wr = Ln.router + (size_t)rrow * H;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
+        }
+        if (is_shared) load_shared_pair<SH>(Ln, sj, lane, sp);
+        if (Ln.nw) nwv = reinterpret_cast<const float4*>(Ln.nw)[tid];
+      }
+
+      // ---- down row n: 8 experts + shared, weighted, plus the residual
+      float xa[32], xb[32], xc[8], suma = 0.f, sumb = 0.f, sumc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float4 v = as4[i * 64 + lane], w = as4[512 + i * 64 + lane];
+        xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+        xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+        suma += (v.x + v.y) + (v.z + v.w);
+        sumb += (w.x + w.y) + (w.z + w.w);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float4 v = as4[1024 + i * 64 + lane];
+        xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
+        sumc += (v.x + v.y) + (v.z + v.w);
+      }
+      float da = 0.f, db = 0.f;
+      da = dot8_q4(qa.x, xa + 0, da), db = dot8_q4(qb.x, xb + 0, db);
+      da = dot8_q4(qa.y, xa + 8, da), db = dot8_q4(qb.y, xb + 8, db);
+      da = dot8_q4(qa.z, xa + 16, da), db = dot8_q4(qb.z, xb + 16, db);
+      da = dot8_q4(qa.w, xa + 24, da), db = dot8_q4(qb.w, xb + 24, db);
+      float dc = dot4_u8b(qs.x, xc, 0.f);
+      dc = dot4_u8b(qs.y, xc + 4, dc);
+      const float2 pa = SC::pair(da_s), pb = SC::pair(db_s);
+      float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) + sgv * ssc * (dc - 128.f * sumc);
+      acc = wave_sum(acc);
+      if (lane == 0) {
+        const float y = res + acc;
+        if (l + 1 < L) ll_put(ll + LL_X + n, y, tC);
+        else x[n] = y;
+        if (xs_out) xs_out[(size_t)l * H + n] = y;
+      }
+      nws[tid] = nwv;  // the next layer's norm weight (the router rows read nws before the logits barrier)
+      ST_MARK(6);
+      // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
+      if (poller && l + 1 < L) {
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync);
+        if (!r && lane == 0) s_abort = 1;
+        ST_PUT(10, r);
+      }
+    }
+    __syncthreads();
+    ST_MARK(7);
+    if (s_abort) return;
+  }
+  if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The grid needs all ST_NB workgroups resident at once; checked once per device.
+int step_grid_ok(const void* kernel) {
+  static int ok[64] = {0};  // 0 unknown, 1 yes, -1 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (ok[dev] == 0) {
+    int cus = 0, per = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, ST_NT, 0);
+    ok[dev] = (cus * per >= ST_NB) ? 1 : -1;
+  }
+  return ok[dev] == 1;
+}
+
+template <class SC, class SH>
+int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, int I, int topk, float eps,
+                uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out, float* xs_out,
+                hipStream_t st) {
+  if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || L < 1 || L > ST_MAXL) return -1;
+  if (!layers || !x || !ll || !sync) return -1;
+  const void* k = reinterpret_cast<const void*>(&k_decode_step<SC, SH>);
+  if (!step_grid_ok(k)) return -1;
+  hipLaunchKernelGGL((k_decode_step<SC, SH>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
+                     idx_out, wts_out, sgate_out, xs_out);
+  return 0;
+}
+
+}  // namespace
+
+API int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I, int topk,
+                           float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
+                           float* xs_out, dr_stream_t st) {
+  return launch_step<ScaleF16, Q8G128F16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+                                          sgate_out, xs_out, (hipStream_t)st);
+}
+
+API int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I,
+                                 int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
+                                 float* sgate_out, float* xs_out, dr_stream_t st) {
+  return launch_step<ScaleBF16, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+                                           sgate_out, xs_out, (hipStream_t)st);
+}

@@ -213,6 +213,52 @@ int dr_gemv_q4_bf16s(const uint8_t* q, const dr_bf16* sm, const dr_bf16* x, floa
 int dr_gemv_q8_bf16s(const int8_t* w, const dr_bf16* s, const float* x, const float* res, float* y, int n,
                      int k, const float* nw, float eps, dr_stream_t st);
 
+/* ===================================================================================== */
+/* Fused multi-layer decode step (persistent kernel) -- no single reference symbol: it    */
+/* replaces the per-layer chain dr_router_topk + dr_moe_decode that src/engine.rs:1001-   */
+/* 1007 records for every MoE layer of a decode step (src/ffi.rs:41-46).                  */
+/* ===================================================================================== */
+
+/* Per-layer weight pointers, an array of n_layers of these in DEVICE memory.  Formats as in
+ * dr_moe_decode (reference: f16 scales, int8 group 128) or dr_moe_decode_bf16s (bf16 scales,
+ * per-channel int8 scales); router is the bf16 [E+1, H] matrix whose row E is the
+ * shared-expert gate; nw is the RMSNorm weight (+1 folded in) or NULL for no norm. */
+typedef struct dr_decode_layer {
+  const dr_bf16* router;
+  const float* nw;
+  const uint8_t* gu_q;
+  const void* gu_s;
+  const uint8_t* d_q;
+  const void* d_s;
+  const int8_t* sgu_q;
+  const uint16_t* sgu_s;
+  const int8_t* sd_q;
+  const uint16_t* sd_s;
+} dr_decode_layer;
+
+/* 64-bit words of the exchange buffer `ll` of dr_moe_decode_step*. */
+#define DR_STEP_LL_WORDS 6920
+
+/* One token through n_layers MoE layers in one launch (h = 2048, i = 512, topk = 8,
+ * 8 <= e <= 256, 1 <= n_layers <= 1365):  for each layer, x = x + MoE(RMSNorm(x)) with the
+ * same router, top-k, expert and shared-expert arithmetic as dr_router_topk followed by
+ * dr_moe_decode(x, res = x, y = x); routing is bit-exact with that chain.
+ *   x         f32 [h], read at launch and overwritten with the last layer's output;
+ *   ll        u64 [DR_STEP_LL_WORDS] exchange buffer, sync u32 [4]: both zeroed once by the
+ *             caller before the first call and then left alone (a call advances sync[0]);
+ *             sync[1] != 0 reports that a call timed out waiting for its workgroups (every
+ *             later call then returns at once until the caller zeroes sync and ll again);
+ *   idx_out i32 [n_layers*8], wts_out f32 [n_layers*8], sgate_out f32 [n_layers],
+ *   xs_out f32 [n_layers*h]: optional (NULL) per-layer routing and layer outputs.
+ * Needs 256 co-resident workgroups of 512 threads (one MI355X); returns -1 otherwise.  Calls
+ * sharing one ll/sync pair must be stream ordered. */
+int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i, int topk,
+                       float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
+                       float* xs_out, dr_stream_t st);
+int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
+                             int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
+                             float* sgate_out, float* xs_out, dr_stream_t st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,7 +14,8 @@
  *   or_exp              against libm exp in double (<= 2 ulp), special values
  *   or_rmsnorm_canon,
  *   or_dot_bf16_canon   against float64 sums (tight bound) and exact small-integer cases
- *   or_softmax_topk     one-hot, all-equal (ties -> lowest indices), E == topk, brute-force sort
+ *   or_softmax_topk     one-hot, all-equal (ties -> lowest indices), E == topk, brute-force sort,
+ *                       weights against float64 softmax
  *   or_moe_group        histogram / exclusive scan / stable-permutation invariants, brute force
  *   or_moe_decode       dense float64 matmul restatement (numpy), single-expert == SwiGLU MLP,
  *                       expert-storage permutation invariance, zero expert
@@ -208,37 +209,50 @@ void or_router_logits(const uint16_t* W, const float* xn, int rows, int K, float
   for (int r = 0; r < rows; ++r) logits[r] = or_dot_bf16_canon(W + (size_t)r * K, xn, K);
 }
 
-/* Softmax over E logits + top-k with (p desc, index asc) and renormalised weights
- * (kernels/drama.cu:322-367, 398-431).  z: lane l sums exp over experts l + 64 j in order,
- * then the butterfly.  p = ex / z.  total accumulates the picked p in pick order. */
+/* Top-k selection key of a logit: an int in the float order of the logit (negative values
+ * have their magnitude bits flipped, so -0 sorts just below +0); NaN logits rank below
+ * every number, picked experts below those. */
+#define KEY_PAD INT32_MIN
+#define KEY_PICKED (INT32_MIN + 1)
+#define KEY_NAN (INT32_MIN + 2)
+static int32_t logit_key(float v) {
+  if (v != v) return KEY_NAN;
+  const int32_t i = (int32_t)f2u(v);
+  return i >= 0 ? i : i ^ 0x7fffffff;
+}
+
+/* Top-k of E logits with softmax-renormalised weights (kernels/drama.cu:322-367,398-431;
+ * selection on the logits as src/mlx/engine.rs:249-258 does -- exp is monotone, so the
+ * logit order is the probability order).  Selection: k rounds of (key desc, index asc).
+ * m = max of the non-NaN logits; z: lane l sums exp(l - m) over experts l + 64 j in order,
+ * then the butterfly; p_k = exp(l_k - m) / z; total = sum of p_k in pick order;
+ * wts_k = p_k / total. */
 int or_softmax_topk(const float* l, int E, int topk, int* idx, float* wts) {
   if (E < 1 || E > 256 || topk < 1 || topk > E || topk > 32) return -1;
   float m = -INFINITY;
   for (int e = 0; e < E; ++e) m = l[e] > m ? l[e] : m;
-  float ex[256], p[256], a[64];
-  for (int e = 0; e < 256; ++e) ex[e] = e < E ? or_exp(l[e] - m) : 0.f;
+  float a[64];
   for (int ln = 0; ln < 64; ++ln) {
     float s = 0.f;
-    for (int j = 0; j < 4; ++j) s = s + ex[ln + 64 * j];
+    for (int j = 0; j < 4; ++j) {
+      const int e = ln + 64 * j;
+      s = s + (e < E ? or_exp(l[e] - m) : 0.f);
+    }
     a[ln] = s;
   }
   const float z = tree64(a);
-  /* selection keys: p, -1 for a NaN probability, -2 once picked; the best starts at -4, so
-   * every round picks a distinct expert below E whatever the logits hold */
-  for (int e = 0; e < 256; ++e) {
-    const float q = ex[e] / z;
-    p[e] = e < E ? (q != q ? -1.f : q) : -3.f;
-  }
+  int32_t key[256];
+  for (int e = 0; e < E; ++e) key[e] = logit_key(l[e]);
   float total = 0.f;
   for (int k = 0; k < topk; ++k) {
     int bi = 0;
-    float bv = -4.f;
+    int32_t bk = KEY_PAD;
     for (int e = 0; e < E; ++e)
-      if (p[e] > bv) bv = p[e], bi = e; /* strict > keeps the lowest index on ties */
+      if (key[e] > bk) bk = key[e], bi = e; /* strict > keeps the lowest index on ties */
     idx[k] = bi;
-    wts[k] = bv;
-    total = total + bv;
-    p[bi] = -2.f;
+    key[bi] = KEY_PICKED;
+    wts[k] = or_exp(l[bi] - m) / z;
+    total = total + wts[k];
   }
   for (int k = 0; k < topk; ++k) wts[k] = wts[k] / total;
   return 0;

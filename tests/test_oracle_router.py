@@ -74,10 +74,8 @@ def test_softmax_topk_brute_force():
         if trial % 5 == 0:
             l = np.round(l * 2) / 2  # many exact ties
         idx, w = O.softmax_topk(l, E, topk)
-        # the oracle's own probabilities, recomputed with its exp: selection must be the
-        # (p desc, index asc) order of those
-        ex = O.exp(l - l.max())
-        order = sorted(range(E), key=lambda e: (-float(ex[e]), e))[:topk]
+        # selection is the (logit desc, index asc) order, -0 just below +0
+        order = sorted(range(E), key=lambda e: (-float(l[e]), bool(np.signbit(l[e])), e))[:topk]
         np.testing.assert_array_equal(idx, order)
         p = np.exp(l.astype(np.float64) - l.max())
         p /= p.sum()
@@ -130,13 +128,24 @@ def test_group_invariants_and_brute_force():
         np.testing.assert_array_equal(slot_of, expect)
 
 
+def test_softmax_topk_signed_zero_and_infinities():
+    """-0 ranks just below +0 (key order), -inf is a number above NaN; weights stay exact."""
+    l = np.full(16, -np.inf, np.float32)
+    l[3], l[9] = -0.0, 0.0
+    idx, w = O.softmax_topk(l, 16, 3)
+    assert list(idx) == [9, 3, 0]
+    np.testing.assert_array_equal(w, np.array([0.5, 0.5, 0.0], np.float32))
+
+
 def test_softmax_topk_nan_logits_pick_distinct_valid_experts():
-    """NaN probabilities rank below every real one, never leave [0, E) and never repeat."""
+    """NaN logits rank below every number, picks never leave [0, E) and never repeat."""
     for E in (256, 16, 8):
         l = np.full(E, np.nan, np.float32)
         idx, w = O.softmax_topk(l, E, 8)
         np.testing.assert_array_equal(idx, np.arange(8))
         l = np.random.default_rng(E).normal(0, 1, E).astype(np.float32)
-        l[[1, 3]] = np.nan  # one NaN poisons the max and the sum: every p is NaN
+        l[[1, 3]] = np.nan  # NaN poisons the sum (every weight is NaN), not the selection
         idx, w = O.softmax_topk(l, E, 8)
         assert len(set(idx.tolist())) == 8 and idx.min() >= 0 and idx.max() < E
+        if E > 10:
+            assert 1 not in idx and 3 not in idx

@@ -34,6 +34,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true", help="skip configurations 1, 4 and 5")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the fused-step timing (no parity, per-layer chain, extras or CPU leg): "
+                         "the run that rocprofv3 --pmc / --kernel-trace profiles")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only a 1 GiB device-to-device copy, 5 times: calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -82,6 +87,53 @@ def layer_decode_bytes(L):
     return router + TOPK * per_expert + shared + vec
 
 
+def measured_traffic():
+    """HBM bytes per k_decode_step launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy of known size)."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", "k_decode_step_cfg3_pmc.txt")):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def time_chain(args, lib, st, sp, step):
+    """The engine's per-layer launches (3 kernels per layer), eager and graph-replayed."""
+    import torch
+
+    for _ in range(args.warmup):
+        step()
+    st.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(st)
+    for _ in range(args.steps):
+        step()
+    ev1.record(st)
+    torch.cuda.synchronize()
+    eager_ms = ev0.elapsed_time(ev1) / args.steps
+
+    # ---- graph timing: one captured step, replayed
+    gexec = ctypes.c_void_p()
+    lib.dr_graph_begin(sp)
+    step()
+    lib.dr_graph_end(sp, ctypes.byref(gexec))
+    for _ in range(args.warmup):
+        lib.dr_graph_launch(gexec, sp)
+    st.synchronize()
+    torch.cuda.synchronize()
+    ev0.record(st)
+    for _ in range(args.steps):
+        lib.dr_graph_launch(gexec, sp)
+    ev1.record(st)
+    torch.cuda.synchronize()
+    graph_ms = ev0.elapsed_time(ev1) / args.steps
+    lib.dr_graph_destroy(gexec)
+    return eager_ms, graph_ms
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -89,6 +141,15 @@ def main():
               "note (DESIGN.md), not a measured configuration", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.calib_copy:
+        src = torch.ones(1 << 28, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4, "launches": 5}))
+        return
     import dramamoe as D
 
     lib = D.lib()
@@ -141,8 +202,10 @@ def main():
 
     # ---- parity spot check: layer 0 of the first step against the CPU oracle
     parity = None
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     try:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        if args.profile:
+            raise RuntimeError("skipped (--profile)")
         import numpy as np
         import oracle as O
 
@@ -169,6 +232,8 @@ def main():
     # router on the step's own layer inputs; full-layer outputs of the first and last layer
     fparity = None
     try:
+        if args.profile:
+            raise RuntimeError("skipped (--profile)")
         x_start = x.cpu().numpy().copy()
         fused_step(outputs=True)
         st.synchronize()
@@ -224,40 +289,15 @@ def main():
     lib.dr_graph_destroy(fexec)
     fused_ok = int(sync[1].item()) == 0
 
-    # ---- per-layer kernel chain (router, gate_up, down per layer): eager timing
-    for _ in range(args.warmup):
-        step()
-    st.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(st)
-    for _ in range(args.steps):
-        step()
-    ev1.record(st)
-    torch.cuda.synchronize()
-    eager_ms = ev0.elapsed_time(ev1) / args.steps
-
-    # ---- graph timing: one captured step, replayed
-    gexec = ctypes.c_void_p()
-    lib.dr_graph_begin(sp)
-    step()
-    lib.dr_graph_end(sp, ctypes.byref(gexec))
-    for _ in range(args.warmup):
-        lib.dr_graph_launch(gexec, sp)
-    st.synchronize()
-    torch.cuda.synchronize()
-    ev0.record(st)
-    for _ in range(args.steps):
-        lib.dr_graph_launch(gexec, sp)
-    ev1.record(st)
-    torch.cuda.synchronize()
-    graph_ms = ev0.elapsed_time(ev1) / args.steps
-    lib.dr_graph_destroy(gexec)
+    # ---- per-layer kernel chain (router, gate_up, down per layer): eager and graph timing
+    eager_ms = graph_ms = float("nan")
+    if not args.profile:
+        eager_ms, graph_ms = time_chain(args, lib, st, sp, step)
     ok = bool(torch.isfinite(x).all().item())
 
     # ---- the other benchmark configurations (single GEMV, prefill, FP8 and int8 dense)
     extra = None
-    if not args.no_extra:
+    if not args.no_extra and not args.profile:
         import benchcfg
 
         extra = {}
@@ -272,7 +312,7 @@ def main():
 
     # ---- CPU baseline: the oracle's decode layer on this host's cores (bounded sample)
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.profile:
         try:
             import numpy as np
             import oracle as O
@@ -315,11 +355,12 @@ def main():
                    "layers": nl, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I},
         "fused_graph_ms_per_step": round(fused_graph_ms, 4),
         "fused_graph_us_per_layer": round(fused_graph_ms * 1000.0 / nl, 3),
-        "chain_eager_us_per_layer": round(eager_ms * 1000.0 / nl, 3),
-        "chain_graph_us_per_layer": round(graph_ms * 1000.0 / nl, 3),
+        "chain_eager_us_per_layer": None if args.profile else round(eager_ms * 1000.0 / nl, 3),
+        "chain_graph_us_per_layer": None if args.profile else round(graph_ms * 1000.0 / nl, 3),
         "chain_note": "the engine's per-layer launches dr_router_topk + dr_moe_decode_bf16s (3 kernels per layer)",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/k_decode_step_cfg3_pmc.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
                      "bytes_per_step": bytes_step,
                      "kernel": "k_decode_step (the whole 40-layer step in one launch); achieved = algorithmic "
                                "bytes per step / kernel time from HIP events on its stream"},

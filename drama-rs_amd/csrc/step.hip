@@ -38,6 +38,13 @@ constexpr int ST_H = 2048, ST_I = 512, ST_TOPK = 8, ST_MAXE = 256;
 constexpr int ST_NB = 256, ST_WPB = 8, ST_NT = ST_WPB * 64, ST_NP = 8;  // every wave polls a share
 constexpr uint32_t ST_TAG_STRIDE = 4096;
 constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
+constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the critical path cost ~1 us)
+// Polling too early slows an exchange down: polls of 2048 waves that reach the memory side
+// before the producers' stores contend with them (measured on MI355X, configuration 3: the
+// layer went from 20.3 to 15.8 us with these delays).  So each wave issues its first poll of
+// an exchange this many 10 ns ticks after it reaches the exchange, and waits a little
+// between rounds.
+constexpr uint32_t ST_DLY_LOGITS = 120, ST_DLY_ACT = 200, ST_DLY_X = 120, ST_DLY_ROUND = 20;
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
@@ -82,6 +89,11 @@ DEV float2 ll_val2(uint64_t w) {
   return make_float2(__uint_as_float((uint32_t)(w >> 16) & 0xffffff00u), __uint_as_float((uint32_t)(w << 8)));
 }
 
+DEV void wait_ticks(uint32_t n) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < n) __builtin_amdgcn_s_sleep(1);
+}
+
 // LDS float4 slots: int4 rows give lane l the 32 inputs [32 l, 32 l + 32) -> slot i * 64 + l
 DEV int slot_q4(int f) { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
 // int8 K = 2048 rows give lane l bytes [16 l, +16) and [1024 + 16 l, +16)
@@ -92,8 +104,9 @@ DEV int slot_q8(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
 // current, then hands each to spec.store.  Returns the rounds taken, 0 after ~0.2 s (the
 // caller aborts).
 template <int N, int NP, class Spec>
-DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync) {
+DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync, uint32_t first_delay) {
   const int lane = lane_id();
+  wait_ticks(first_delay);
   const uint64_t* b = base + lane + 64 * p;
   uint64_t v[N];
 #pragma unroll
@@ -112,6 +125,7 @@ DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sy
       if (lane == 0) __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return 0;
     }
+    wait_ticks(ST_DLY_ROUND);
 #pragma unroll
     for (int i = 0; i < N; ++i)
       if (!sp.ok(p + NP * i, v[i])) v[i] = ll_get(b + 64 * NP * i);
@@ -189,6 +203,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ int s_sel[ST_TOPK];
   __shared__ float s_mz[2];
   __shared__ int s_abort;
+  __shared__ dr_decode_layer s_tab[ST_TABL];  // the first ST_TABL layer records
   if (__syncthreads_or(__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) return;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int pw = wave;  // every wave polls rows pw + 8 i of each exchange
@@ -211,7 +226,15 @@ __global__ void __launch_bounds__(ST_NT, 1)
   float4 nwv = make_float4(1.f, 1.f, 1.f, 1.f);
   if (tid == 0) s_abort = 0;
   {
-    const dr_decode_layer L0 = layers[0];
+    const int nw32 = (L < ST_TABL ? L : ST_TABL) * (int)(sizeof(dr_decode_layer) / 4);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(layers);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(s_tab);
+    for (int i = tid; i < nw32; i += ST_NT) dst[i] = src[i];
+  }
+  __syncthreads();
+  auto layer = [&](int i) { return i < ST_TABL ? s_tab[i] : layers[i]; };
+  {
+    const dr_decode_layer L0 = layer(0);
     if (is_router) {
       const uint16_t* wr = L0.router + (size_t)rrow * H;
 #pragma unroll
@@ -225,7 +248,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __syncthreads();
 
   for (int l = 0; l < L; ++l) {
-    const dr_decode_layer Ly = layers[l];
+    const dr_decode_layer Ly = layer(l);
     const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2;
     ST_MARK(0);
     float res;  // x[n], read now: the poller overwrites xr4 during the down phase
@@ -256,7 +279,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(1);
     }
     if (poller) {
-      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync);
+      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, ST_DLY_LOGITS);
       if (!r && lane == 0) s_abort = 1;
       ST_PUT(8, r);
     }
@@ -362,7 +385,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4)}, sync);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4)}, sync, ST_DLY_ACT);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -376,7 +399,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       // ---- next layer's known weights: issued after the activation poll (a wave's loads
       // return in order, so loads issued before a poll would delay it)
       if (l + 1 < L) {
-        const dr_decode_layer Ln = layers[l + 1];
+        const dr_decode_layer Ln = layer(l + 1);
         if (is_router) {
           const uint16_t* wr = Ln.router + (size_t)rrow * H;
 #pragma unroll
@@ -422,7 +445,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
-        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync);
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, ST_DLY_X);
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }

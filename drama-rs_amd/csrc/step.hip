@@ -96,8 +96,6 @@ DEV void wait_ticks(uint32_t n) {
 
 // LDS float4 slots: int4 rows give lane l the 32 inputs [32 l, 32 l + 32) -> slot i * 64 + l
 DEV int slot_q4(int f) { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
-// int8 K = 2048 rows give lane l bytes [16 l, +16) and [1024 + 16 l, +16)
-DEV int slot_q8(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
 
 // Wave share of an exchange: wave p of NP owns, in lane l, the words base[l + 64 r] of rows
 // r = p + NP i, i < N.  It reloads the words whose tag is not yet the phase's until all are
@@ -197,7 +195,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   constexpr int H = ST_H, I = ST_I;
   __shared__ float4 xr4[H / 4];                        // residual stream x (raw)
   __shared__ float4 nws[H / 4];                        // RMSNorm weight of the layer
-  __shared__ float4 xq4[H / 4], xq8[H / 4];            // normalised x in the int4 / int8 lane slots
+  __shared__ float4 xq4[H / 4];                        // normalised x in the int4 lane slots
   __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
   __shared__ float lg[ST_MAXE + 1];
   __shared__ int s_sel[ST_TOPK];
@@ -261,9 +259,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       for (int j = 0; j < 8; ++j) xr[j] = xr4[lane + 64 * j];
       const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
       {
-        const float4 xn = canon_norm4(xr4[tid], inv, nwv);
-        xq4[slot_q4(tid)] = xn;
-        xq8[slot_q8(tid)] = xn;
+        xq4[slot_q4(tid)] = canon_norm4(xr4[tid], inv, nwv);
       }
       if (is_router) {
         float4 a[4], b[4];
@@ -275,6 +271,31 @@ __global__ void __launch_bounds__(ST_NT, 1)
         }
         const float acc = canon_row_dot<4>(rw.w, a, b);
         if (lane == 0) ll_put(ll + LL_LOG + rrow, acc, tA);
+      }
+      // shared gate_up pair (waves 2 and 6): needs only the normalised x, so it runs here,
+      // inside the logits exchange, instead of after top-k
+      if (is_shared) {
+        float xa[16], xb[16], sa = 0.f, sb = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int f = 4 * lane + i;
+          const float4 v = canon_norm4(xr4[f], inv, nws[f]), w = canon_norm4(xr4[256 + f], inv, nws[256 + f]);
+          xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+          xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+          sa += (v.x + v.y) + (v.z + v.w);
+          sb += (w.x + w.y) + (w.z + w.w);
+        }
+        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
+        const uint32_t gw0[4] = {sp.g0.x, sp.g0.y, sp.g0.z, sp.g0.w}, gw1[4] = {sp.g1.x, sp.g1.y, sp.g1.z, sp.g1.w};
+        const uint32_t uw0[4] = {sp.u0.x, sp.u0.y, sp.u0.z, sp.u0.w}, uw1[4] = {sp.u1.x, sp.u1.y, sp.u1.z, sp.u1.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          ga = dot4_u8b(gw0[d], xa + 4 * d, ga), gb = dot4_u8b(gw1[d], xb + 4 * d, gb);
+          ua = dot4_u8b(uw0[d], xa + 4 * d, ua), ub = dot4_u8b(uw1[d], xb + 4 * d, ub);
+        }
+        const float gv = wave_sum(sp.sg0 * (ga - 128.f * sa) + sp.sg1 * (gb - 128.f * sb));
+        const float uv = wave_sum(sp.su0 * (ua - 128.f * sa) + sp.su1 * (ub - 128.f * sb));
+        if (lane == 0) ll_put(ll + LL_ACT + ST_TOPK * I / 2 + sj, silu(gv) * uv, tB);
       }
       ST_MARK(1);
     }
@@ -333,7 +354,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
       const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
 
-      // ---- gate_up: two routed pairs per wave, one shared pair on waves 2 and 6
+      // ---- gate_up: two routed pairs per wave
       {
         float xv[32], xsum = 0.f;
 #pragma unroll
@@ -356,28 +377,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
           av[p] = silu(gv) * uv;
         }
         if (lane == 0) ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
-      }
-      if (is_shared) {
-        float xa[16], xb[16], sa = 0.f, sb = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 v = xq8[i * 64 + lane], w = xq8[256 + i * 64 + lane];
-          xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
-          xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-          sa += (v.x + v.y) + (v.z + v.w);
-          sb += (w.x + w.y) + (w.z + w.w);
-        }
-        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
-        const uint32_t gw0[4] = {sp.g0.x, sp.g0.y, sp.g0.z, sp.g0.w}, gw1[4] = {sp.g1.x, sp.g1.y, sp.g1.z, sp.g1.w};
-        const uint32_t uw0[4] = {sp.u0.x, sp.u0.y, sp.u0.z, sp.u0.w}, uw1[4] = {sp.u1.x, sp.u1.y, sp.u1.z, sp.u1.w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          ga = dot4_u8b(gw0[d], xa + 4 * d, ga), gb = dot4_u8b(gw1[d], xb + 4 * d, gb);
-          ua = dot4_u8b(uw0[d], xa + 4 * d, ua), ub = dot4_u8b(uw1[d], xb + 4 * d, ub);
-        }
-        const float gv = wave_sum(sp.sg0 * (ga - 128.f * sa) + sp.sg1 * (gb - 128.f * sb));
-        const float uv = wave_sum(sp.su0 * (ua - 128.f * sa) + sp.su1 * (ub - 128.f * sb));
-        if (lane == 0) ll_put(ll + LL_ACT + ST_TOPK * I / 2 + sj, silu(gv) * uv, tB);
       }
       ST_MARK(4);
 

@@ -159,6 +159,44 @@ DEV int canon_select_topk(const float* __restrict__ l, int E, int topk) {
   return id;
 }
 
+// The same selection in two phases for topk <= 8 and E <= 256, spread over four waves.
+// Phase 1, wave w (w < 4): the top-8 of experts [64 w, 64 w + 64) (one per lane), in pick
+// order; lane r < 8 returns pick r as (key, expert).  Phase 2, one wave: lane c < 32 holds
+// candidate c = 8 w + r; the top-k of the 32 candidates is the top-k of all E experts (each
+// group contributes at most 8), and among equal keys a lower candidate slot always holds the
+// lower expert (within a group equal keys are picked in index order, groups are in index
+// order), so lowest slot first reproduces (key desc, index asc).  Lane k < topk returns the
+// expert of pick k.
+DEV void canon_select_group8(const float* __restrict__ l, int E, int w, int* cand_key, int* cand_e) {
+  const int lane = lane_id();
+  const int e = 64 * w + lane;
+  int key = e < E ? canon_logit_key(l[e]) : KEY_PAD;
+  int ck = KEY_PAD, ce = 0;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int kb = wave_max_i(key);
+    const int ls = (int)__builtin_ctzll(__ballot(key == kb));
+    if (lane == ls) key = KEY_PICKED;
+    if (lane == r) ck = kb, ce = 64 * w + ls;
+  }
+  *cand_key = ck;
+  *cand_e = ce;
+}
+
+DEV int canon_merge_topk32(int key, int e, int topk) {
+  const int lane = lane_id();
+  if (lane >= 32) key = KEY_PAD;
+  int id = 0;
+  for (int k = 0; k < topk; ++k) {
+    const int kb = wave_max_i(key);
+    const int ls = (int)__builtin_ctzll(__ballot(key == kb));
+    const int eb = __builtin_amdgcn_readlane(e, ls);
+    if (lane == ls) key = KEY_PICKED;
+    if (lane == k) id = eb;
+  }
+  return id;
+}
+
 // Softmax denominator: m = max of the non-NaN logits, z = sum of canon_exp(l - m) with lane
 // l summing experts l + 64 j in order, then the xor butterfly.  Same bits on every lane.
 DEV float canon_softmax_z(const float* __restrict__ l, int E, float* m_out) {

@@ -199,6 +199,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
   __shared__ float lg[ST_MAXE + 1];
   __shared__ int s_sel[ST_TOPK];
+  __shared__ int2 s_cand[32];
   __shared__ float s_mz[2];
   __shared__ int s_abort;
   __shared__ dr_decode_layer s_tab[ST_TABL];  // the first ST_TABL layer records
@@ -308,14 +309,22 @@ __global__ void __launch_bounds__(ST_NT, 1)
     ST_MARK(2);
     if (s_abort) return;
 
-    // ---- top-k: selection on wave 0 and the softmax denominator on wave 1, side by side
-    if (wave == 0) {
-      const int id = canon_select_topk(lg, E, ST_TOPK);
-      if (lane < ST_TOPK) s_sel[lane] = id;
-    } else if (wave == 1) {
+    // ---- top-k: per-group top-8 on waves 0..3 and the softmax denominator on wave 4 side
+    // by side, then the merge of the 32 candidates on wave 0
+    if (wave < 4) {
+      int ck, ce;
+      canon_select_group8(lg, E, wave, &ck, &ce);
+      if (lane < 8) s_cand[wave * 8 + lane] = make_int2(ck, ce);
+    } else if (wave == 4) {
       float m;
       const float z = canon_softmax_z(lg, E, &m);
       if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int2 c = s_cand[lane & 31];
+      const int id = canon_merge_topk32(c.x, c.y, ST_TOPK);
+      if (lane < ST_TOPK) s_sel[lane] = id;
     }
     __syncthreads();
 

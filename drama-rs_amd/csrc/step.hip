@@ -132,6 +132,7 @@ DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sy
   for (int i = 0; i < N; ++i) {
     const int r = p + NP * i;
     if (sp.valid(r, lane + 64 * r)) sp.store(r, lane + 64 * r, v[i]);
+    sp.post(r, v[i]);  // whole wave
   }
   return it;
 }
@@ -145,13 +146,15 @@ struct Spec32 {
   DEV uint64_t ready(int) const { return (uint64_t)tag << 32; }
   DEV bool ok(int, uint64_t v) const { return (uint32_t)(v >> 32) == tag; }
   DEV void store(int, int w, uint64_t v) const { dst[w] = __uint_as_float((uint32_t)v); }
+  DEV void post(int, uint64_t) const {}
 };
 
 // activations: words 0..2047 hold routed elements 2w, 2w + 1 (packed, i < 32), words
 // 2048..2559 shared element w - 2048 (one per word, i >= 32); stored into the down slots
 struct SpecAct {
   uint32_t tag;
-  float* dst;  // as4 as floats
+  float* dst;   // as4 as floats
+  float* sums;  // [0, 128): sums of the 32-element routed chunks, [128, 192): of the 8-element shared chunks
   DEV bool valid(int r, int) const { return r < 40; }
   DEV uint64_t ready(int i) const { return i < 32 ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32; }
   DEV bool ok(int i, uint64_t v) const {
@@ -165,6 +168,21 @@ struct SpecAct {
     } else {
       const int e = w - 2048;
       dst[(1024 + ((e >> 2) & 1) * 64 + (e >> 3)) * 4 + (e & 3)] = __uint_as_float((uint32_t)v);
+    }
+  }
+  // chunk sums for the down dot's min term: a routed chunk is 16 consecutive words (lanes) of
+  // one row, a shared chunk 8 consecutive words
+  DEV void post(int r, uint64_t v) const {
+    const int lane = lane_id();
+    if (r < 32) {
+      const float2 p = ll_val2(v);
+      float t = p.x + p.y;
+      t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t);
+      if ((lane & 15) == 0) sums[4 * r + (lane >> 4)] = t;
+    } else {
+      float t = __uint_as_float((uint32_t)v);
+      t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
+      if ((lane & 7) == 0) sums[128 + 8 * (r - 32) + (lane >> 3)] = t;
     }
   }
 };
@@ -199,6 +217,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
   __shared__ float lg[ST_MAXE + 1];
   __shared__ int s_sel[ST_TOPK];
+  __shared__ float s_asum[192];  // activation chunk sums (see SpecAct::post)
+  __shared__ float s_xsum[64];   // sums of the 32-input chunks of xn (lane l's chunk)
   __shared__ int2 s_cand[32];
   __shared__ float s_mz[2];
   __shared__ int s_abort;
@@ -260,7 +280,11 @@ __global__ void __launch_bounds__(ST_NT, 1)
       for (int j = 0; j < 8; ++j) xr[j] = xr4[lane + 64 * j];
       const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
       {
-        xq4[slot_q4(tid)] = canon_norm4(xr4[tid], inv, nwv);
+        const float4 xn = canon_norm4(xr4[tid], inv, nwv);
+        xq4[slot_q4(tid)] = xn;
+        float t = (xn.x + xn.y) + (xn.z + xn.w);  // threads 8c..8c+7 hold chunk c
+        t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
+        if ((lane & 7) == 0) s_xsum[tid >> 3] = t;
       }
       if (is_router) {
         float4 a[4], b[4];
@@ -365,12 +389,12 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
       // ---- gate_up: two routed pairs per wave
       {
-        float xv[32], xsum = 0.f;
+        float xv[32];
+        const float xsum = s_xsum[lane];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float4 v = xq4[i * 64 + lane];
           xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
-          xsum += (v.x + v.y) + (v.z + v.w);
         }
         float av[2];
 #pragma unroll
@@ -393,7 +417,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4)}, sync, ST_DLY_ACT);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4), s_asum}, sync, ST_DLY_ACT);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -418,20 +442,18 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
 
       // ---- down row n: 8 experts + shared, weighted, plus the residual
-      float xa[32], xb[32], xc[8], suma = 0.f, sumb = 0.f, sumc = 0.f;
+      float xa[32], xb[32], xc[8];
+      const float suma = s_asum[lane], sumb = s_asum[64 + lane], sumc = s_asum[128 + lane];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float4 v = as4[i * 64 + lane], w = as4[512 + i * 64 + lane];
         xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
         xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-        suma += (v.x + v.y) + (v.z + v.w);
-        sumb += (w.x + w.y) + (w.z + w.w);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const float4 v = as4[1024 + i * 64 + lane];
         xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
-        sumc += (v.x + v.y) + (v.z + v.w);
       }
       float da = 0.f, db = 0.f;
       da = dot8_q4(qa.x, xa + 0, da), db = dot8_q4(qb.x, xb + 0, db);

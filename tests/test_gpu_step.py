@@ -92,8 +92,11 @@ def test_step_repeats_and_matches_first_call_bits():
 
 
 def test_step_without_norm_and_without_outputs():
+    # without the norm the activations grow with |x| (N(0,1) inputs give layer outputs of
+    # 1e4 whose small elements are differences of 1e4-sized sums, beyond any fp32 tolerance
+    # relative to the element); inputs of scale 0.05 keep the comparison meaningful
     st = Stack([77, 78], 32, "cfg", with_norm=False)
-    x0 = np.random.default_rng(8).normal(0, 1, H).astype(np.float32)
+    x0 = (0.05 * np.random.default_rng(8).normal(0, 1, H)).astype(np.float32)
     xa, xb = dev(x0), dev(x0)
     r = st.run(xa)
     check_stack(st, x0, *r, host(xa))

@@ -52,10 +52,17 @@ struct FmtQ4 {
   static DEV size_t row_bytes(int K) { return (size_t)K / 2; }
   // fragment bytes of (row, group G) for lane group g: 8 bytes = 16 nibbles
   static DEV void load(const uint8_t* row, int G, int g, uint2& raw) { raw = ld8(row + G * 32 + g * 8); }
+  // word j of a fragment = (nibble j, nibble j + 4) as bf16 (128 + q): one v_and_or_b32 per
+  // word ((w >> 4 j) & 0x000f000f | 0x43004300; the compiler does not fuse the and/or)
+  static DEV uint32_t nib2(uint32_t w, uint32_t m, uint32_t b) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(m), "v"(b));
+    return r;
+  }
   static DEV void convert(const uint2& raw, uint4& a0, uint4& a1) {
     const uint32_t m = 0x000f000fu, b = 0x43004300u;
-    a0 = make_uint4((raw.x & m) | b, ((raw.x >> 4) & m) | b, ((raw.x >> 8) & m) | b, ((raw.x >> 12) & m) | b);
-    a1 = make_uint4((raw.y & m) | b, ((raw.y >> 4) & m) | b, ((raw.y >> 8) & m) | b, ((raw.y >> 12) & m) | b);
+    a0 = make_uint4(nib2(raw.x, m, b), nib2(raw.x >> 4, m, b), nib2(raw.x >> 8, m, b), nib2(raw.x >> 12, m, b));
+    a1 = make_uint4(nib2(raw.y, m, b), nib2(raw.y >> 4, m, b), nib2(raw.y >> 8, m, b), nib2(raw.y >> 12, m, b));
   }
   // (scale, min) of row n, group G: raw word, then decoded
   static DEV uint32_t scale_raw(const void* S, size_t n, int G, int K) {
@@ -229,16 +236,23 @@ __global__ void __launch_bounds__(PF_WPB * 64)
           f32x4 xg = z;
           if (F::has_min) xg = mfma(x1, ones, mfma(x0, ones, z));
           const float2 pa = F::scale_val(sa.sc[i]);
+          const float ca = pa.y - 128.f * pa.x;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) tA[r] += F::has_min ? pa.x * accA[r] + (pa.y - 128.f * pa.x) * xg[r] : pa.x * accA[r];
+          for (int r = 0; r < 4; ++r) {
+            tA[r] = __builtin_fmaf(pa.x, accA[r], tA[r]);
+            if (F::has_min) tA[r] = __builtin_fmaf(ca, xg[r], tA[r]);
+          }
           if (MODE == 0) {
             uint4 b0, b1;
             F::convert(sbb.raw[i], b0, b1);
             const f32x4 accB = mfma(x1, b1, mfma(x0, b0, z));
             const float2 pb = F::scale_val(sbb.sc[i]);
+            const float cb = pb.y - 128.f * pb.x;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              tB[r] += F::has_min ? pb.x * accB[r] + (pb.y - 128.f * pb.x) * xg[r] : pb.x * accB[r];
+            for (int r = 0; r < 4; ++r) {
+              tB[r] = __builtin_fmaf(pb.x, accB[r], tB[r]);
+              if (F::has_min) tB[r] = __builtin_fmaf(cb, xg[r], tB[r]);
+            }
           }
         }
       }

@@ -52,17 +52,10 @@ struct FmtQ4 {
   static DEV size_t row_bytes(int K) { return (size_t)K / 2; }
   // fragment bytes of (row, group G) for lane group g: 8 bytes = 16 nibbles
   static DEV void load(const uint8_t* row, int G, int g, uint2& raw) { raw = ld8(row + G * 32 + g * 8); }
-  // word j of a fragment = (nibble j, nibble j + 4) as bf16 (128 + q): one v_and_or_b32 per
-  // word ((w >> 4 j) & 0x000f000f | 0x43004300; the compiler does not fuse the and/or)
-  static DEV uint32_t nib2(uint32_t w, uint32_t m, uint32_t b) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(m), "v"(b));
-    return r;
-  }
   static DEV void convert(const uint2& raw, uint4& a0, uint4& a1) {
     const uint32_t m = 0x000f000fu, b = 0x43004300u;
-    a0 = make_uint4(nib2(raw.x, m, b), nib2(raw.x >> 4, m, b), nib2(raw.x >> 8, m, b), nib2(raw.x >> 12, m, b));
-    a1 = make_uint4(nib2(raw.y, m, b), nib2(raw.y >> 4, m, b), nib2(raw.y >> 8, m, b), nib2(raw.y >> 12, m, b));
+    a0 = make_uint4((raw.x & m) | b, ((raw.x >> 4) & m) | b, ((raw.x >> 8) & m) | b, ((raw.x >> 12) & m) | b);
+    a1 = make_uint4((raw.y & m) | b, ((raw.y >> 4) & m) | b, ((raw.y >> 8) & m) | b, ((raw.y >> 12) & m) | b);
   }
   // (scale, min) of row n, group G: raw word, then decoded
   static DEV uint32_t scale_raw(const void* S, size_t n, int G, int K) {

@@ -18,8 +18,8 @@ constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
 // loads of a wave (its weight row, x for the norm, x and nw for its dot lanes) are issued
 // before any arithmetic.  Logits are published with cache-bypassing (sc1) stores; after its
 // stores have completed (s_waitcnt) each block counts itself in with one relaxed atomic, and
-// the last block reads the logits back with sc1 loads and runs softmax/top-k with its first
-// wave.  No cache-maintenance fence is needed: every cross-block value bypasses the
+// the last block reads the logits back with sc1 loads and runs softmax/top-k (two-phase
+// selection on four waves for topk <= 8).  No cache-maintenance fence is needed: every cross-block value bypasses the
 // non-coherent caches.  The last block resets the counter for the next call.
 template <int K>
 __global__ void __launch_bounds__(RT_WPB * 64)
@@ -64,16 +64,37 @@ __global__ void __launch_bounds__(RT_WPB * 64)
   if (threadIdx.x == 0)
     s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
-  if (!s_last || wave != 0) return;
-  // stage the logits (sc1 loads) into registers of wave 0, then the canonical softmax/top-k
+  if (!s_last) return;
+  // stage the logits (sc1 loads) in LDS, then the canonical softmax/top-k: for topk <= 8 the
+  // group selections on waves 0..3 and the denominator on wave 4 run side by side
   __shared__ float lg[257];
-  for (int e = lane; e <= E; e += WAVE) lg[e] = __hip_atomic_load(logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  int my_idx;
-  float my_w;
-  canon_softmax_topk(lg, E, topk, &my_idx, &my_w);
-  if (lane < topk) idx[lane] = my_idx, wts[lane] = my_w;
+  __shared__ int2 s_cand[32];
+  __shared__ float s_mz[2];
+  if ((int)threadIdx.x <= E) lg[threadIdx.x] = __hip_atomic_load(logits + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (topk <= 8) {
+    if (wave < 4) {
+      int ck, ce;
+      canon_select_group8(lg, E, wave, &ck, &ce);
+      if (lane < 8) s_cand[wave * 8 + lane] = make_int2(ck, ce);
+    } else if (wave == 4) {
+      float m;
+      const float z = canon_softmax_z(lg, E, &m);
+      if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int2 c = s_cand[lane & 31];
+    const int id = canon_merge_topk32(c.x, c.y, topk);
+    const float w = canon_topk_weight(lg[lane < topk ? id : 0], s_mz[0], s_mz[1], topk);
+    if (lane < topk) idx[lane] = id, wts[lane] = w;
+  } else {
+    if (wave != 0) return;
+    int my_idx;
+    float my_w;
+    canon_softmax_topk(lg, E, topk, &my_idx, &my_w);
+    if (lane < topk) idx[lane] = my_idx, wts[lane] = my_w;
+  }
   if (lane == 0) {
     sgate[0] = lg[E];
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

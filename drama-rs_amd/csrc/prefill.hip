@@ -282,14 +282,175 @@ __global__ void __launch_bounds__(PF_WPB * 64)
   }
 }
 
-// grid x: experts (grouped) or 1 (fixed_rows >= 0); y: 16-row tiles / PF_WPB; z: token passes
+
+// K-split variant, used for the shared expert (one weight set over all rows; for the grouped
+// experts it measured slower than k_grouped).  Block = RT consecutive 16-row tiles of weight rows (gate_up: 16 gate +
+// 16 up rows per tile) of one expert; wave w owns the input groups [GPW w, GPW (w + 1)) of
+// every row, so each wave issues all loads of a tile at once, and the next tile's weights
+// stream in while the current one is used.  Per row tile the weights stay in registers for
+// every 16-token tile of the expert (tiles blockIdx.z, + gridDim.z, ...); a wave reads its
+// slice of the 16 tokens straight from global memory (no LDS staging), runs the exact-dequant
+// MFMA steps, and the eight partial 16 x 16 tiles are summed through LDS in wave order.
+template <class F>
+struct Wts {
+  typename Raw<F>::T a, b;
+  uint32_t sa, sb;
+};
+
+template <class F, int MODE, int K>
+DEV void load_tile(const uint8_t* wq, const char* ws, size_t rb, int half, int r0, int G0, int g, int c16,
+                   Wts<F> (&w)[K / 64 / PF_WPB]) {
+  constexpr int GPW = K / 64 / PF_WPB;
+  const size_t nA = (size_t)(r0 + c16), nB = (size_t)(half + r0 + c16);
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    F::load(wq + nA * rb, G0 + i, g, w[i].a);
+    if (MODE == 0) F::load(wq + nB * rb, G0 + i, g, w[i].b);
+    if (F::scale_group != 0) {
+      w[i].sa = F::scale_raw(ws, nA, G0 + i, K);
+      if (MODE == 0) w[i].sb = F::scale_raw(ws, nB, G0 + i, K);
+    }
+  }
+}
+
+template <class F, int MODE, int K>
+__global__ void __launch_bounds__(PF_WPB * 64)
+    k_grouped_ks(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
+                 const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
+                 size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int fixed_rows, int RT) {
+  constexpr int NG = K / 64, GPW = NG / PF_WPB;
+  static_assert(GPW * PF_WPB == NG, "groups per wave");
+  __shared__ float red[PF_WPB][8][64];
+  const int e = fixed_rows >= 0 ? 0 : blockIdx.x;
+  const int cnt = fixed_rows >= 0 ? fixed_rows : counts[e];
+  const int tiles = (cnt + PF_TOK - 1) / PF_TOK;
+  if ((int)blockIdx.z >= tiles) return;
+  const size_t off = fixed_rows >= 0 ? 0 : (size_t)offsets[e];
+  const int lane = lane_id(), wave = wave_id();
+  const int g = lane >> 4, c16 = lane & 15;
+  const int half = MODE == 0 ? N / 2 : 0;
+  const uint8_t* wq = Wq + (size_t)e * expert_q_bytes;
+  const char* ws = reinterpret_cast<const char*>(Ws) + (size_t)e * expert_s_elems * s_elem_bytes;
+  const size_t rb = F::row_bytes(K);
+  const int G0 = wave * GPW;
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  Wts<F> cur[GPW], nxt[GPW];
+  load_tile<F, MODE, K>(wq, ws, rb, half, blockIdx.y * RT * 16, G0, g, c16, cur);
+  for (int t = 0; t < RT; ++t) {
+    const int r0 = (blockIdx.y * RT + t) * 16;
+    // the next row tile (the last one reloads itself: a conditional load would make the
+    // compiler wait for every outstanding load before using the current tile)
+    load_tile<F, MODE, K>(wq, ws, rb, half, (blockIdx.y * RT + (t + 1 < RT ? t + 1 : t)) * 16, G0, g, c16, nxt);
+    for (int tile = blockIdx.z; tile < tiles; tile += gridDim.z) {
+      // this lane's token row (MFMA A row c16), its 16 inputs 64 G + 16 g .. + 15 per group
+      const int tok = tile * PF_TOK + c16;
+      const uint16_t* xr = X + (off + (size_t)(tok < cnt ? tok : cnt - 1)) * K;
+      uint4 x0[GPW], x1[GPW];
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) {
+        const int k0 = 64 * (G0 + i) + 16 * g;
+        uint4 v0 = ld16(xr + k0), v1 = ld16(xr + k0 + 8);
+        if (tok >= cnt) v0 = v1 = make_uint4(0, 0, 0, 0);
+        // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7)
+        x0[i] = make_uint4(__builtin_amdgcn_perm(v0.z, v0.x, 0x05040100u), __builtin_amdgcn_perm(v0.z, v0.x, 0x07060302u),
+                           __builtin_amdgcn_perm(v0.w, v0.y, 0x05040100u), __builtin_amdgcn_perm(v0.w, v0.y, 0x07060302u));
+        x1[i] = make_uint4(__builtin_amdgcn_perm(v1.z, v1.x, 0x05040100u), __builtin_amdgcn_perm(v1.z, v1.x, 0x07060302u),
+                           __builtin_amdgcn_perm(v1.w, v1.y, 0x05040100u), __builtin_amdgcn_perm(v1.w, v1.y, 0x07060302u));
+      }
+      f32x4 tA = z, tB = z;
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) {
+        uint4 a0, a1;
+        F::convert(cur[i].a, a0, a1);
+        if (F::scale_group == 0) {
+          tA = mfma(x1[i], a1, mfma(x0[i], a0, tA));
+          if (MODE == 0) {
+            uint4 b0, b1;
+            F::convert(cur[i].b, b0, b1);
+            tB = mfma(x1[i], b1, mfma(x0[i], b0, tB));
+          }
+        } else {
+          const f32x4 accA = mfma(x1[i], a1, mfma(x0[i], a0, z));
+          f32x4 xg = z;
+          if (F::has_min) xg = mfma(x1[i], ones, mfma(x0[i], ones, z));
+          const float2 pa = F::scale_val(cur[i].sa);
+          const float ca = pa.y - 128.f * pa.x;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            tA[r] = __builtin_fmaf(pa.x, accA[r], tA[r]);
+            if (F::has_min) tA[r] = __builtin_fmaf(ca, xg[r], tA[r]);
+          }
+          if (MODE == 0) {
+            uint4 b0, b1;
+            F::convert(cur[i].b, b0, b1);
+            const f32x4 accB = mfma(x1[i], b1, mfma(x0[i], b0, z));
+            const float2 pb = F::scale_val(cur[i].sb);
+            const float cb = pb.y - 128.f * pb.x;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              tB[r] = __builtin_fmaf(pb.x, accB[r], tB[r]);
+              if (F::has_min) tB[r] = __builtin_fmaf(cb, xg[r], tB[r]);
+            }
+          }
+        }
+      }
+      // sum the eight K slices in wave order; lane (token 4 g + r, row c16) of every wave
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        red[wave][r][lane] = tA[r];
+        if (MODE == 0) red[wave][4 + r][lane] = tB[r];
+      }
+      __syncthreads();
+      const int ll = threadIdx.x & 63, rr = threadIdx.x >> 6;
+      if (rr < 4) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int w = 0; w < PF_WPB; ++w) {
+          a += red[w][rr][ll];
+          if (MODE == 0) b += red[w][4 + rr][ll];
+        }
+        const int tk = tile * PF_TOK + 4 * (ll >> 4) + rr, row = ll & 15;
+        if (tk < cnt) {
+          float rsA = 1.f, rsB = 1.f;
+          if (F::scale_group == 0) {
+            rsA = F::scale(ws, (size_t)(r0 + row), 0, K).x;
+            if (MODE == 0) rsB = F::scale(ws, (size_t)(half + r0 + row), 0, K).x;
+          }
+          const size_t slot = off + tk;
+          if (MODE == 0)
+            reinterpret_cast<uint16_t*>(out)[slot * (size_t)(N / 2) + r0 + row] = to_bf16(silu(a * rsA) * (b * rsB));
+          else
+            reinterpret_cast<float*>(out)[slot * (size_t)N + r0 + row] = a * rsA;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) cur[i] = nxt[i];
+  }
+}
+
 template <class F>
 void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const int* offsets, const int* counts,
                     void* out, int E, int N, int K, int mode, size_t eq, size_t es, int sb, int fixed_rows,
                     hipStream_t st) {
   const int rows_out = mode == 0 ? N / 2 : N;
-  const int passes = fixed_rows >= 0 ? (fixed_rows + PF_TOK - 1) / PF_TOK : PF_ZPASS;
-  const dim3 grid(fixed_rows >= 0 ? 1 : E, (rows_out / 16 + PF_WPB - 1) / PF_WPB, passes);
+  if (fixed_rows >= 0) {
+    // one weight set over all rows (the shared expert): the K-split kernel, one 16-row tile
+    // per block, token tiles over grid z (measured 2x faster than k_grouped here)
+    const int tiles = (fixed_rows + PF_TOK - 1) / PF_TOK;
+    const dim3 grid(1, rows_out / 16, tiles < 8 ? tiles : 8);
+    if (mode == 0)
+      hipLaunchKernelGGL((k_grouped_ks<F, 0, 2048>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out,
+                         N, eq, es, sb, fixed_rows, 1);
+    else
+      hipLaunchKernelGGL((k_grouped_ks<F, 1, 512>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out, N,
+                         eq, es, sb, fixed_rows, 1);
+    return;
+  }
+  // grouped experts: one expert per grid x, 16-row tiles / PF_WPB over y, token passes over z
+  const dim3 grid(E, (rows_out / 16 + PF_WPB - 1) / PF_WPB, PF_ZPASS);
   const size_t lds = (size_t)PF_TOK * K * 2;
   if (mode == 0)
     hipLaunchKernelGGL((k_grouped<F, 0, 2048>), grid, dim3(PF_WPB * 64), lds, st, wq, ws, X, offsets, counts, out, N,

@@ -321,7 +321,7 @@ def main():
             O.lib().or_set_threads(threads)
             xs = x0
             n, t_cpu = 0, 0.0
-            while t_cpu < args.cpu_seconds and n < 400:
+            while t_cpu < args.cpu_seconds and n < 5000:
                 t1 = time.perf_counter()
                 _, ri, rw, rs = O.router_topk(h["router"].view(np.uint16), xs, h["nw"], 1e-6, E, TOPK)
                 _, xs = O.moe_decode(hl, xs, ri, rw, rs, xs, H, I, TOPK, nw=h["nw"], eps=1e-6)

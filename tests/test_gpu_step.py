@@ -114,3 +114,38 @@ def test_step_rejects_bad_shapes():
         a = list(base)
         a[pos] = bad
         assert L.raw("dr_moe_decode_step_bf16s")(*a) == -1
+
+
+def test_step_graph_replays_match_eager():
+    """One captured launch replayed several times, with eager work and synchronisations in
+    between: every replay must give the eager call's bits (the step only reads its own slots'
+    tags, so replays need no reset)."""
+    import ctypes
+
+    import torch
+
+    st = Stack([61, 62], 64, "cfg")
+    x0 = np.random.default_rng(9).normal(0, 1, H).astype(np.float32)
+    ref = dev(x0)
+    st.run(ref)
+    want = host(ref).copy()
+    L = D.lib()
+    s = torch.cuda.Stream()
+    xg = torch.zeros(H, device="cuda")
+    sp = s.cuda_stream
+    g = ctypes.c_void_p()
+    L.dr_graph_begin(sp)
+    L.dr_moe_decode_step_bf16s(D.ptr(st.table), 2, D.ptr(xg), 64, H, I, TOPK, 1e-6, D.ptr(st.ll), D.ptr(st.sync),
+                               None, None, None, None, sp)
+    L.dr_graph_end(sp, ctypes.byref(g))
+    try:
+        for rep in range(4):
+            xg.copy_(torch.from_numpy(x0).cuda())
+            torch.cuda.synchronize()
+            L.dr_graph_launch(g, sp)
+            s.synchronize()
+            np.testing.assert_array_equal(bits(host(xg)), bits(want), err_msg=f"replay {rep}")
+            st.run(dev(x0))  # eager call in between advances the same epoch counter
+        assert int(host(st.sync)[1]) == 0
+    finally:
+        L.dr_graph_destroy(g)

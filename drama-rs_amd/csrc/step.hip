@@ -379,13 +379,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
       const size_t ea = (size_t)__shfl(my_idx, ka), eb = (size_t)__shfl(my_idx, 4 + ka);
       const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
-      const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
-      const uint4 qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
-      const uint4 qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
-      const uint32_t da_s = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
-      const uint32_t db_s = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
-      const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
-      const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
 
       // ---- gate_up: two routed pairs per wave
       {
@@ -412,6 +405,15 @@ __global__ void __launch_bounds__(ST_NT, 1)
         if (lane == 0) ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
       }
       ST_MARK(4);
+      // down rows (8 experts + shared): issued after the gate_up stores so the gate_up stream
+      // has the bandwidth to itself; they land during the activation exchange's first delay
+      const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
+      const uint4 qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
+      const uint4 qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
+      const uint32_t da_s = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
+      const uint32_t db_s = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
+      const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
+      const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
 
       // ---- activation exchange, collected by the poller
       ST_MARKW(14, 2);

@@ -44,7 +44,7 @@ constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the
 // layer went from 20.3 to 15.8 us with these delays).  So each wave issues its first poll of
 // an exchange this many 10 ns ticks after it reaches the exchange, and waits a little
 // between rounds.
-constexpr uint32_t ST_DLY_LOGITS = 120, ST_DLY_ACT = 200, ST_DLY_X = 120, ST_DLY_ROUND = 20;
+constexpr uint32_t ST_DLY_LOGITS = 120, ST_DLY_ACT = 160, ST_DLY_X = 120, ST_DLY_ROUND = 20;
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer

@@ -1,0 +1,156 @@
+"""Loader for the MoE weights of a converted drama-rs checkpoint ("drama-rs-v1").
+
+Reads the directory layout the reference's converter writes and its Rust loader reads
+(tools/convert.py:224-263,345-346; src/model.rs:186-291): ``drama.json`` (format name, int4
+and int8 group sizes, the model config) and one ``layerNN.safetensors`` per decoder layer with
+
+    post_norm                 f32  [H]             RMSNorm weight of the MoE input (+1 folded in)
+    moe.router                bf16 [E + 1, H]      router rows, row E = shared-expert gate
+    moe.gate_up.q4 / .sm      u8 [E, 2I, H/2] / f16 [E, 2I, H/64, 2]
+    moe.down.q4 / .sm         u8 [E, H, I/2]  / f16 [E, H, I/64, 2]
+    moe.shared_gate_up.q8/.s  i8 [2I, H]      / f16 [2I, H/128]
+    moe.shared_down.q8 / .s   i8 [H, I]       / f16 [H, I/128]
+
+Only the MoE tensors are read (attention, DeltaNet and the audio tower are outside this
+library).  Dtypes and shapes are checked the way src/model.rs:193-230 checks them, with the
+same "layerNN.name: dtype X, expected Y" style errors.  ``MoeStack`` uploads the layers to the
+GPU and drives the fused decode step (dr_moe_decode_step, reference f16 formats) or the
+per-layer chain (dr_router_topk + dr_moe_decode) over them.
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import dramamoe
+
+FORMAT = "drama-rs-v1"
+Q4_GROUP, Q8_GROUP = 64, 128
+LL_WORDS = 6920  # DR_STEP_LL_WORDS
+
+
+class CheckpointError(ValueError):
+    pass
+
+
+def read_meta(path: str) -> dict:
+    with open(os.path.join(path, "drama.json")) as f:
+        meta = json.load(f)
+    if meta.get("format") != FORMAT or meta.get("q4_group") != Q4_GROUP or meta.get("q8_group") != Q8_GROUP:
+        raise CheckpointError(f"unsupported converted format in {path}")
+    tc = meta["config"]["text_config"]
+    for k in ("hidden_size", "num_hidden_layers", "num_experts", "num_experts_per_tok", "moe_intermediate_size"):
+        if k not in tc:
+            raise CheckpointError(f"drama.json: text_config.{k} missing")
+    return meta
+
+
+def _expect(prefix, name, t, dtype, shape):
+    import torch
+
+    if t.dtype != dtype:
+        raise CheckpointError(f"{prefix}{name}: dtype {t.dtype}, expected {dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise CheckpointError(f"{prefix}{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    return t.contiguous() if isinstance(t, torch.Tensor) else t
+
+
+def read_layer(path: str, i: int, tc: dict) -> dict:
+    """Host tensors (torch, CPU) of layer i's MoE, checked against the config."""
+    import torch
+    from safetensors import safe_open
+
+    H, E, I = tc["hidden_size"], tc["num_experts"], tc["moe_intermediate_size"]
+    prefix = f"layer{i:02d}."
+    fn = os.path.join(path, f"layer{i:02d}.safetensors")
+    out = {}
+    with safe_open(fn, framework="pt", device="cpu") as f:
+        names = set(f.keys())
+
+        def get(name, dtype, shape):
+            if name not in names:
+                raise CheckpointError(f"{prefix}{name}: not in {os.path.basename(fn)}")
+            return _expect(prefix, name, f.get_tensor(name), dtype, shape)
+
+        out["nw"] = get("post_norm", torch.float32, (H,))
+        out["router"] = get("moe.router", torch.bfloat16, (E + 1, H))
+        out["gu_q"] = get("moe.gate_up.q4", torch.uint8, (E, 2 * I, H // 2))
+        out["gu_s"] = get("moe.gate_up.sm", torch.float16, (E, 2 * I, H // Q4_GROUP, 2))
+        out["d_q"] = get("moe.down.q4", torch.uint8, (E, H, I // 2))
+        out["d_s"] = get("moe.down.sm", torch.float16, (E, H, I // Q4_GROUP, 2))
+        out["sgu_q"] = get("moe.shared_gate_up.q8", torch.int8, (2 * I, H))
+        out["sgu_s"] = get("moe.shared_gate_up.s", torch.float16, (2 * I, H // Q8_GROUP))
+        out["sd_q"] = get("moe.shared_down.q8", torch.int8, (H, I))
+        out["sd_s"] = get("moe.shared_down.s", torch.float16, (H, I // Q8_GROUP))
+    return out
+
+
+def write_layer(path: str, i: int, tensors: dict) -> None:
+    """Write layer i's MoE tensors under the reference's names (for tests and tools that make
+    synthetic checkpoints); ``tensors`` uses the keys read_layer returns."""
+    from safetensors.torch import save_file
+
+    names = {"nw": "post_norm", "router": "moe.router", "gu_q": "moe.gate_up.q4", "gu_s": "moe.gate_up.sm",
+             "d_q": "moe.down.q4", "d_s": "moe.down.sm", "sgu_q": "moe.shared_gate_up.q8",
+             "sgu_s": "moe.shared_gate_up.s", "sd_q": "moe.shared_down.q8", "sd_s": "moe.shared_down.s"}
+    save_file({names[k]: v.contiguous() for k, v in tensors.items()}, os.path.join(path, f"layer{i:02d}.safetensors"))
+
+
+def write_meta(path: str, H: int, E: int, I: int, layers: int, topk: int = 8, eps: float = 1e-6) -> None:
+    tc = {"hidden_size": H, "num_hidden_layers": layers, "num_experts": E, "num_experts_per_tok": topk,
+          "moe_intermediate_size": I, "shared_expert_intermediate_size": I, "rms_norm_eps": eps}
+    with open(os.path.join(path, "drama.json"), "w") as f:
+        json.dump({"format": FORMAT, "q4_group": Q4_GROUP, "q8_group": Q8_GROUP, "config": {"text_config": tc}}, f,
+                  indent=1)
+
+
+_KEYS = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")  # dr_decode_layer order
+
+
+class MoeStack:
+    """The MoE layers of a converted checkpoint resident on the GPU."""
+
+    def __init__(self, path: str, layers: list[int] | None = None, device: str = "cuda"):
+        import torch
+
+        meta = read_meta(path)
+        self.tc = tc = meta["config"]["text_config"]
+        self.H, self.E, self.I = tc["hidden_size"], tc["num_experts"], tc["moe_intermediate_size"]
+        self.topk = tc["num_experts_per_tok"]
+        self.eps = float(tc.get("rms_norm_eps", 1e-6))
+        ids = list(range(tc["num_hidden_layers"])) if layers is None else list(layers)
+        self.layers = [{k: v.to(device) for k, v in read_layer(path, i, tc).items()} for i in ids]
+        tab = [[L[k].data_ptr() for k in _KEYS] for L in self.layers]
+        self.table = torch.tensor(tab, dtype=torch.int64, device=device)
+        self.ll = torch.zeros(LL_WORDS, dtype=torch.int64, device=device)
+        self.sync = torch.zeros(4, dtype=torch.int32, device=device)
+        self.lib = dramamoe.lib()
+
+    def step(self, x, stream=None, idx_out=None, wts_out=None, sgate_out=None, xs_out=None) -> None:
+        """x (f32 [H], device) through every loaded layer in one fused launch, in place."""
+        P = dramamoe.ptr
+        self.lib.dr_moe_decode_step(P(self.table), len(self.layers), P(x), self.E, self.H, self.I, self.topk, self.eps,
+                                    P(self.ll), P(self.sync), P(idx_out), P(wts_out), P(sgate_out), P(xs_out),
+                                    stream if stream is not None else dramamoe.stream_ptr())
+        if int(self.sync[1].item()) != 0:
+            raise dramamoe.DramaMoeError("dr_moe_decode_step timed out waiting for its workgroups")
+
+    def chain(self, x, stream=None) -> None:
+        """The same layers through the engine's per-layer launches (router, then decode)."""
+        import torch
+
+        P = dramamoe.ptr
+        st = stream if stream is not None else dramamoe.stream_ptr()
+        dev = x.device
+        logits = torch.empty(self.E + 1, device=dev)
+        idx = torch.empty(self.topk, dtype=torch.int32, device=dev)
+        wts = torch.empty(self.topk, device=dev)
+        sg = torch.empty(1, device=dev)
+        counter = torch.zeros(4, dtype=torch.int32, device=dev)
+        act = torch.empty((self.topk + 1) * self.I, device=dev)
+        for L in self.layers:
+            self.lib.dr_router_topk(P(L["router"]), P(x), P(L["nw"]), self.eps, P(logits), self.E, self.topk, self.H,
+                                    P(idx), P(wts), P(sg), P(counter), None, None, None, None, 0, 0, 0, 0, st)
+            self.lib.dr_moe_decode(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]),
+                                   P(L["sd_q"]), P(L["sd_s"]), P(x), P(idx), P(wts), P(sg), P(x), P(act), P(x), self.H,
+                                   self.I, self.topk, P(L["nw"]), self.eps, None, 0, st)

@@ -14,8 +14,8 @@ and int8 group sizes, the model config) and one ``layerNN.safetensors`` per deco
 Only the MoE tensors are read (attention, DeltaNet and the audio tower are outside this
 library).  Dtypes and shapes are checked the way src/model.rs:193-230 checks them, with the
 same "layerNN.name: dtype X, expected Y" style errors.  ``MoeStack`` uploads the layers to the
-GPU and drives the fused decode step (dr_moe_decode_step, reference f16 formats) or the
-per-layer chain (dr_router_topk + dr_moe_decode) over them.
+GPU and drives the fused decode step (dr_moe_decode_step, reference f16 formats), the
+per-layer chain (dr_router_topk + dr_moe_decode) or the chunked prefill over them.
 """
 from __future__ import annotations
 
@@ -134,6 +134,45 @@ class MoeStack:
                                     stream if stream is not None else dramamoe.stream_ptr())
         if int(self.sync[1].item()) != 0:
             raise dramamoe.DramaMoeError("dr_moe_decode_step timed out waiting for its workgroups")
+
+    def prefill(self, l: int, x, hn, chunk: int = 1024, stream=None) -> None:
+        """Prefill of loaded layer l for rows token rows (the engine's moe_prefill,
+        src/engine.rs:544-604): x f32 [rows, H] residual stream updated in place, hn bf16
+        [rows, H] its RMSNorm.  Rows go in chunks of at most `chunk` (grouping handles up to
+        8192 (row, expert) pairs per call): router GEMM, top-k, shared expert, device-side
+        grouping, gather, grouped expert GEMMs and the weighted combine, no host round trip."""
+        import ctypes
+
+        import torch
+
+        P = dramamoe.ptr
+        L, lib = self.layers[l], self.lib
+        st = stream if stream is not None else dramamoe.stream_ptr()
+        rows = x.shape[0]
+        H, E, I, k = self.H, self.E, self.I, self.topk
+        if chunk * k > 8192:
+            raise ValueError("chunk * topk must be <= 8192")
+        c = min(chunk, rows)
+        dev = x.device
+        z = lambda n, dt=torch.float32: torch.empty(n, dtype=dt, device=dev)
+        logits, idx, wts, sg = z(c * (E + 1)), z(c * k, torch.int32), z(c * k), z(c)
+        sact, sh = z(c * I, torch.int16), z(c * H)
+        counts, offsets, slot_of = z(E, torch.int32), z(E, torch.int32), z(c * k, torch.int32)
+        xp, act, yp = z(c * k * H, torch.int16), z(c * k * I, torch.int16), z(c * k * H)
+        h = ctypes.c_void_p()
+        lib.dr_cublas_create(ctypes.byref(h), st)
+        for r0 in range(0, rows, c):
+            n = min(c, rows - r0)
+            hr, xr = hn[r0:r0 + n], x[r0:r0 + n]
+            lib.dr_gemm(h.value, P(hr), P(L["router"]), P(logits), n, E + 1, H, 0.0)
+            lib.dr_moe_topk(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), st)
+            lib.dr_moe_shared_prefill(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(hr), n, P(sact),
+                                      P(sh), H, I, st)
+            lib.dr_moe_group(P(idx), n * k, E, P(counts), P(offsets), P(slot_of), st)
+            lib.dr_moe_gather_rows(P(slot_of), n, k, P(hr), P(xp), H, st)
+            lib.dr_moe_prefill(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(xp), P(offsets), P(counts),
+                               P(act), P(yp), E, H, I, st)
+            lib.dr_moe_combine(P(xr), P(yp), P(slot_of), P(wts), P(sg), P(sh), n, k, H, st)
 
     def chain(self, x, stream=None) -> None:
         """The same layers through the engine's per-layer launches (router, then decode)."""

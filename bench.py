@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--profile", action="store_true",
                     help="only the fused-step timing (no parity, per-layer chain, extras or CPU leg): "
                          "the run that rocprofv3 --pmc / --kernel-trace profiles")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="only configuration 4 (prefill, 8 resident layers): the run profiled for the grouped GEMM")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only a 1 GiB device-to-device copy, 5 times: calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
@@ -153,6 +155,15 @@ def main():
     import dramamoe as D
 
     lib = D.lib()
+    if args.profile_prefill:
+        import benchcfg
+
+        layers = [make_layer_gpu(None, l) for l in range(8)]
+        st = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        benchcfg.config4_prefill(lib, layers, st)  # warm-up pass (clocks, caches of the code objects)
+        print(json.dumps({"cfg4_prefill_int4": benchcfg.config4_prefill(lib, layers, st)}))
+        return
     torch.cuda.set_device(0)
     nl = args.layers
     t0 = time.time()

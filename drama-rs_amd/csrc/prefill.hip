@@ -32,10 +32,11 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int PF_WPB = 8;     // waves per block
+constexpr int PF_WPB = 8;     // waves per block (k_grouped_ks)
+constexpr int PF_GWPB = 8;    // waves per block (k_grouped)
 constexpr int PF_TOK = 16;    // tokens per pass (one MFMA tile)
-constexpr int PF_ZPASS = 4;   // passes of one expert that run concurrently (grid z)
 constexpr int PF_MAXE = 256;  // experts
+constexpr int PF_DEPTH = 4;   // 4-group weight steps in flight per wave (k_grouped)
 
 DEV f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
@@ -48,6 +49,7 @@ DEV f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
 template <class SC>
 struct FmtQ4 {
   static constexpr bool has_min = true;
+  static constexpr bool paired = true;  // k_grouped: 16-byte loads covering two groups per row
   static constexpr int scale_group = 64;  // inputs per scale
   static DEV size_t row_bytes(int K) { return (size_t)K / 2; }
   // fragment bytes of (row, group G) for lane group g: 8 bytes = 16 nibbles
@@ -70,6 +72,7 @@ struct FmtQ4 {
 template <class SH>
 struct FmtQ8 {
   static constexpr bool has_min = false;
+  static constexpr bool paired = false;
   static constexpr int scale_group = SH::per_row ? 0 : 128;
   static DEV size_t row_bytes(int K) { return (size_t)K; }
   static DEV void load(const uint8_t* row, int G, int g, uint4& raw) { raw = ld16(row + G * 64 + g * 16); }
@@ -96,6 +99,7 @@ struct FmtQ8 {
 template <int SF>
 struct FmtFP8 {
   static constexpr bool has_min = false;
+  static constexpr bool paired = false;
   static constexpr int scale_group = 128;
   static DEV size_t row_bytes(int K) { return (size_t)K; }
   static DEV void load(const uint8_t* row, int G, int g, uint4& raw) { raw = ld16(row + G * 64 + g * 16); }
@@ -136,149 +140,368 @@ struct Raw<FmtFP8<SF>> {
   using T = uint4;
 };
 
-// Stage tokens [row0, row0 + ntok) x all K inputs of a bf16 row matrix into LDS in the
-// permuted fragment order: 16-byte block r of token t at t * K / 8 + (r ^ t), the xor spreading the 16
-// tokens of one read over distinct LDS banks; rows beyond ntok are zero.
-DEV void stage_tokens(const uint16_t* __restrict__ X, size_t row0, int ntok, int K, uint4* xs) {
-  const int blk = PF_TOK * K / 8;
-  for (int b = threadIdx.x; b < blk; b += PF_WPB * 64) {
-    const int t = b / (K / 8), r = b % (K / 8);
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (t < ntok) v = ld16(X + (row0 + t) * (size_t)K + r * 8);
-    // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7)
-    xs[b ^ (t & 15)] = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                       __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
-  }
+// Token tile of tokens [row0, row0 + ntok) x all K inputs of a bf16 row matrix, staged into LDS
+// in the permuted fragment order: 16-byte block r of token t at t * K / 8 + (r ^ t), the xor
+// spreading the 16 tokens of one read over distinct LDS banks; rows beyond ntok are zero.
+// Split in two so the caller can issue its first weight loads between the token loads and
+// the LDS stores: the stores wait only for the token loads issued before those weight loads.
+// Workgroup barrier that orders LDS only: global loads in flight stay in flight across it.
+DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// per-lane weight data of 4 consecutive 64-input groups: raw fragments and (scale, min) pairs
-template <class F>
+template <int K, int NT>
+struct TokTile {
+  static constexpr int NB = PF_TOK * K / 8 / NT;  // 16-byte blocks per thread (NT threads)
+  static_assert(NB >= 1 && NB * NT == PF_TOK * K / 8, "token tile split");
+  uint4 v[NB];
+  DEV void load(const uint16_t* __restrict__ X, size_t row0, int ntok) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int b = threadIdx.x + i * NT, t = b / (K / 8), r = b % (K / 8);
+      // rows past ntok load row0 again (straight-line code keeps the load counter exact) and are zeroed
+      const uint4 w = ld16(X + (row0 + (t < ntok ? t : 0)) * (size_t)K + r * 8);
+      v[i] = t < ntok ? w : make_uint4(0, 0, 0, 0);
+    }
+  }
+  // with_sums: also the fp32 sum of every 64-input group of every token, at float index
+  // PF_TOK K / 2 + 16 G + t (after the tile), for the min term of the int4 format
+  DEV void store(uint4* xs, bool with_sums) const {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int b = threadIdx.x + i * NT, t = b / (K / 8);
+      if (with_sums) {
+        // 8 chunks of a group sit in 8 consecutive lanes (K / 8 and the stride are multiples of 8)
+        float sum = 0.f;
+        const uint32_t wv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sum += __uint_as_float(wv[k] << 16) + __uint_as_float(wv[k] & 0xffff0000u);
+        sum = xsum_step<4>(xsum_step<2>(xsum_step<1>(sum)));
+        const int r = b % (K / 8);
+        if ((r & 7) == 0) reinterpret_cast<float*>(xs + PF_TOK * K / 8)[16 * (r >> 3) + t] = sum;
+      }
+      // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7)
+      xs[b ^ (t & 15)] =
+          make_uint4(__builtin_amdgcn_perm(v[i].z, v[i].x, 0x05040100u), __builtin_amdgcn_perm(v[i].z, v[i].x, 0x07060302u),
+                     __builtin_amdgcn_perm(v[i].w, v[i].y, 0x05040100u), __builtin_amdgcn_perm(v[i].w, v[i].y, 0x07060302u));
+    }
+  }
+};
+
+// per-lane weight data of 4 consecutive 64-input groups: raw fragments and (scale, min) pairs.
+// Unpaired formats: raw[i] = this lane's fragment bytes of group G0 + i.  Paired (int4): the
+// four lanes of a row read the 64 bytes of groups (G0 + 2 p, G0 + 2 p + 1) as 16 bytes each,
+// raw[p] = bytes 16 g of that span: lanes g = 0, 1 hold the first group, g = 2, 3 the second
+// (one 64-byte run per row per load: half the cache-line requests of 8-byte loads); all four
+// (scale, min) words of the step come in one 16-byte load.
+template <class F, bool P = F::paired>
 struct Step {
   typename Raw<F>::T raw[4];
   uint32_t sc[4];
 };
+template <class F>
+struct Step<F, true> {
+  uint4 raw[2];
+  uint4 sc;
+};
 
 template <class F>
 DEV void load_step(const uint8_t* row, const void* ws, size_t n, int G0, int g, int K, Step<F>& s) {
+  if constexpr (F::paired) {
+    s.raw[0] = ld16(row + G0 * 32 + g * 16);
+    s.raw[1] = ld16(row + G0 * 32 + 64 + g * 16);
+    s.sc = ld16(reinterpret_cast<const uint32_t*>(ws) + n * (size_t)(K / 64) + G0);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) F::load(row, G0 + i, g, s.raw[i]);
-  if (F::scale_group != 0) {
+    for (int i = 0; i < 4; ++i) F::load(row, G0 + i, g, s.raw[i]);
+    if (F::scale_group != 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s.sc[i] = F::scale_raw(ws, n, G0 + i, K);
+      for (int i = 0; i < 4; ++i) s.sc[i] = F::scale_raw(ws, n, G0 + i, K);
+    }
   }
+}
+
+// nibbles of one 32-bit word -> bf16 fragment 128 + q in the order 0 4 1 5 2 6 3 7 with
+// m = 0x000f000f, b = 0x43004300; m = b = 0 gives the zero fragment (a lane left out)
+DEV uint4 q4_frag(uint32_t w, uint32_t m, uint32_t b) {
+  return make_uint4((w & m) | b, ((w >> 4) & m) | b, ((w >> 8) & m) | b, ((w >> 12) & m) | b);
 }
 
 // MODE 0: gate_up (row pairs j, I + j; writes bf16 silu(g) u)   MODE 1: down (writes f32)
 //
-// Block = PF_WPB waves, wave w owns weight rows [r0, r0 + 16) (and the matching up rows).  A
-// block pass covers PF_TOK tokens of one expert: the token tile (all K inputs) is staged in LDS
-// once, then each wave streams its rows with weights and scales fetched one 4-group step
-// ahead of the matrix cores.  MFMA operands: A = tokens (lane: token l % 16), B = weights
-// (lane: row l % 16), so D[token 4 (l / 16) + i][row l % 16] sits in lane l: one weight row
-// per lane, one (scale, min) pair per group.  The group input sums X_g come from the same
-// MFMA against a fragment of bf16 ones.  Passes: blockIdx.z, then every gridDim.z-th.
+// Work items: (expert e, 16-token pass p < ceil(counts[e] / 16), row block yb).  A persistent
+// grid of resident blocks walks them (item = blockIdx.x, + gridDim.x, ...).  Each wave owns one
+// 16-row tile of an item: down, rows (yb PF_GWPB + w) 16; gate_up, waves 0 .. W/2 - 1 gate
+// rows (W/2 yb + w) 16 and the other half the matching up rows (W waves per block), the up results handed to the gate waves
+// through LDS at the item boundary.  A wave streams its tile as a sequence of 4-group steps
+// against the item's token tile in LDS; the ring of DEPTH steps in flight runs on across
+// items (the next item's first steps are fetched during the current item's last ones, its
+// tokens just before them), and the tokens are stored into the second of two LDS tile buffers
+// at the boundary, so one barrier per item is the only gap.  MFMA operands: A = tokens (lane: token l % 16),
+// B = weights (lane: row l % 16), so D[token 4 (l / 16) + i][row l % 16] sits in lane l: one
+// weight row per lane, one (scale, min) pair per group.  The group input sums X_g come from an
+// MFMA against bf16 ones (int4: staged with the tokens).
 template <class F, int MODE, int K>
-__global__ void __launch_bounds__(PF_WPB * 64)
+__global__ void __launch_bounds__(PF_GWPB * 64)
     k_grouped(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
               const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
-              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int fixed_rows) {
-  extern __shared__ uint4 xs[];  // PF_TOK rows of K / 8 blocks, block r of token t at r ^ t
-  const int e = fixed_rows >= 0 ? 0 : blockIdx.x;
-  const int cnt = fixed_rows >= 0 ? fixed_rows : counts[e];
-  if ((int)blockIdx.z * PF_TOK >= cnt) return;
-  const size_t off = fixed_rows >= 0 ? 0 : (size_t)offsets[e];
+              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int E) {
+  extern __shared__ uint4 xs[];  // two tile buffers of BUF blocks, the item table, the up hand-over
+  constexpr int BUF = PF_TOK * K / 8 + (F::paired ? (K / 64) * PF_TOK / 4 : 0);
+  constexpr int WR = MODE == 0 ? PF_GWPB / 2 : PF_GWPB;  // row tiles per item (per row set)
   const int lane = lane_id(), wave = wave_id();
   const int g = lane >> 4, c16 = lane & 15;
-  const int rows_out = MODE == 0 ? N / 2 : N;
-  const int r0 = (blockIdx.y * PF_WPB + wave) * 16;
-  const bool active = r0 < rows_out;
-  const uint8_t* wq = Wq + (size_t)e * expert_q_bytes;
-  const char* ws = reinterpret_cast<const char*>(Ws) + (size_t)e * expert_s_elems * s_elem_bytes;
-  const size_t rb = F::row_bytes(K);
-  const size_t nA = (size_t)(r0 + c16), nB = (size_t)((MODE == 0 ? N / 2 : 0) + r0 + c16);
-  const uint8_t* rowA = wq + nA * rb;
-  const uint8_t* rowB = wq + nB * rb;
-  constexpr int NG = K / 64;  // 64-input groups; weights run one 4-group step ahead
-  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-  for (int pass = blockIdx.z; pass * PF_TOK < cnt; pass += gridDim.z) {
-    const int t0 = pass * PF_TOK;
-    const int ntok = min(PF_TOK, cnt - t0);
-    __syncthreads();
-    stage_tokens(X, off + t0, ntok, K, xs);
-    __syncthreads();
-    if (!active) continue;
-    f32x4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
-    const uint4* xrow = xs + (size_t)c16 * (K / 8);
-    auto compute = [&](const Step<F>& sa, const Step<F>& sbb, int G0) {
+  const int YB = (MODE == 0 ? N / 2 : N) / (16 * WR);  // row blocks per expert
+  // per lane: pass counts of experts 4 lane + j and their inclusive prefix over all experts;
+  // (end of passes, count, offset) of each kept in LDS; every wave writes the same values and
+  // each lane reads back only its own entries, so no barrier is needed
+  uint4* tbl = xs + 2 * BUF;
+  f32x4* ups = reinterpret_cast<f32x4*>(tbl + 192);  // [2][WR][64] up results (gate_up)
+  int n_pass;
+  {
+    int cl[4], ol[4], pl[4], psum = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int G = G0 + i;
-        const uint4 x0 = xrow[(G * 8 + 2 * g) ^ c16], x1 = xrow[(G * 8 + 2 * g + 1) ^ c16];
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        uint4 a0, a1;
-        F::convert(sa.raw[i], a0, a1);
-        if (F::scale_group == 0) {
-          tA = mfma(x1, a1, mfma(x0, a0, tA));
-          if (MODE == 0) {
-            uint4 b0, b1;
-            F::convert(sbb.raw[i], b0, b1);
-            tB = mfma(x1, b1, mfma(x0, b0, tB));
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      cl[j] = e < E ? counts[e] : 0;
+      ol[j] = e < E ? offsets[e] : 0;
+      pl[j] = (cl[j] + PF_TOK - 1) / PF_TOK;
+      psum += pl[j];
+    }
+    int incl = psum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    n_pass = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));  // wave-uniform, in a scalar register
+    int end = incl - psum, ends[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) end += pl[j], ends[j] = end;
+    tbl[lane] = make_uint4(ends[0], ends[1], ends[2], ends[3]);
+    tbl[64 + lane] = make_uint4(cl[0], cl[1], cl[2], cl[3]);
+    tbl[128 + lane] = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+  }
+  const int n_items = n_pass * YB;
+  struct Item {
+    const uint8_t* wq;
+    const char* ws;
+    size_t row0;  // first token row of the pass
+    int ntok, yb;
+    bool valid;
+  };
+  // item i: flat pass q = i % n_pass (consecutive blocks take consecutive experts), yb = i / n_pass
+  auto item_at = [&](int i) {
+    Item it;
+    it.valid = i < n_items;
+    const int i0 = it.valid ? i : blockIdx.x;  // past the end: a valid item, never computed
+    const int q = i0 % n_pass;
+    it.yb = i0 / n_pass;
+    const uint4 en = tbl[lane], cn = tbl[64 + lane], of = tbl[128 + lane];
+    const int ev[4] = {(int)en.x, (int)en.y, (int)en.z, (int)en.w}, cv[4] = {(int)cn.x, (int)cn.y, (int)cn.z, (int)cn.w};
+    const int ov[4] = {(int)of.x, (int)of.y, (int)of.z, (int)of.w};
+    int me = 0, mp = 0, mc = 0, mo = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = (cv[j] + PF_TOK - 1) / PF_TOK;
+      const bool in = q < ev[j] && q >= ev[j] - p;
+      me = in ? 4 * lane + j : me;
+      mp = in ? q - (ev[j] - p) : mp;
+      mc = in ? cv[j] : mc;
+      mo = in ? ov[j] : mo;
+      found = found || in;
+    }
+    const uint64_t bal = __ballot(found);
+    const int src = bal ? __builtin_ctzll(bal) : 0;
+    const int e = __builtin_amdgcn_readlane(me, src), pass = __builtin_amdgcn_readlane(mp, src);
+    const int cnt = __builtin_amdgcn_readlane(mc, src), o0 = __builtin_amdgcn_readlane(mo, src);
+    it.wq = Wq + (size_t)e * expert_q_bytes;
+    it.ws = reinterpret_cast<const char*>(Ws) + (size_t)e * expert_s_elems * s_elem_bytes;
+    it.row0 = (size_t)o0 + (size_t)pass * PF_TOK;
+    it.ntok = min(PF_TOK, cnt - pass * PF_TOK);
+    return it;
+  };
+  const size_t rb = F::row_bytes(K);
+  constexpr int NS = K / 256;  // 4-group steps per item
+  constexpr int DEPTH = PF_DEPTH < NS ? PF_DEPTH : NS;
+  static_assert(NS % DEPTH == 0, "the ring of steps must divide an item");
+  const bool up = MODE == 0 && wave >= WR;  // gate_up: this wave computes up rows
+  const int wt = wave % WR;
+  // weight row of this lane in item it (gate_up: the up row of an up wave)
+  auto row_of = [&](const Item& it) { return (size_t)(up ? N / 2 : 0) + (size_t)((it.yb * WR + wt) * 16 + c16); };
+  auto fetch = [&](const Item& it, int s, Step<F>& st) {
+    const size_t n = row_of(it);
+    load_step<F>(it.wq + n * rb, it.ws, n, s * 4, g, K, st);
+  };
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  // the int4 conversion constants live in VGPRs: v_and_or_b32 (VOP3) takes no literal
+  // operands on this architecture and at most one scalar one, so with literals the
+  // conversion would cost two instructions per dword instead of one
+  uint32_t q_mask = 0x000f000fu, q_bias = 0x43004300u;
+  asm volatile("" : "+v"(q_mask), "+v"(q_bias));
+  // zero tokens for the int4 pair MFMAs (K / 8 blocks: every offset a pair's read adds stays
+  // inside); each wave writes the whole block itself before its own reads, so no barrier
+  const uint4* zeros = reinterpret_cast<const uint4*>(ups + (MODE == 0 ? 2 * WR * 64 : 0));
+  if (F::paired) {
+    uint4* z = const_cast<uint4*>(zeros);
+    for (int i = lane; i < K / 8; i += 64) z[i] = make_uint4(0, 0, 0, 0);
+  }
+
+  Item cur = item_at(blockIdx.x);
+  if (!cur.valid) return;
+  Item nxt = item_at(blockIdx.x + gridDim.x);
+  Step<F> ring[DEPTH];  // steps in flight
+  TokTile<K, PF_GWPB * 64> tt;
+  {
+    tt.load(X, cur.row0, cur.ntok);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) fetch(cur, d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    tt.store(xs, F::paired);
+  }
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // gate_up: the gate waves finish item k - 1 after the boundary barrier, with the up results
+  // the up waves left in ups[(k - 1) & 1]
+  struct Pending {
+    f32x4 t;
+    size_t row0;
+    int ntok, col;
+    bool valid;
+  } pend;
+  pend.valid = false;
+  auto finish_gate = [&](const Pending& pd, int k1) {
+    const f32x4 u = ups[((k1 & 1) * WR + wt) * 64 + lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = 4 * g + r;
+      if (tok >= pd.ntok) break;
+      reinterpret_cast<uint16_t*>(out)[(pd.row0 + tok) * (size_t)(N / 2) + pd.col] = to_bf16(silu(pd.t[r]) * u[r]);
+    }
+  };
+  int k = 0;
+  for (;; ++k) {
+    if (MODE == 0 && !up && pend.valid) finish_gate(pend, k - 1);
+    const uint4* xb = xs + (k & 1) * BUF;
+    const uint4* xrow = xb + (size_t)c16 * (K / 8);
+    // int4 pairs: lanes g = 0, 1 carry the first group of a pair, g = 2, 3 the second; for the
+    // MFMA of one group the other lanes read the zero block instead of their tokens
+    const uint4* xa_base[4];
+    const uint4* xb_base[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4* own = xrow + ((4 * g + j) ^ c16);
+      xa_base[j] = g < 2 ? own : zeros;
+      xb_base[j] = g < 2 ? zeros : own;
+    }
+    f32x4 tA = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Step<F>& sa, int G0) {
+      if constexpr (F::paired) {
+        const float4* xsum4 = reinterpret_cast<const float4*>(xb + PF_TOK * K / 8);
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const int P = G0 / 2 + pp;
+          const float4 Xa = xsum4[(G0 + 2 * pp) * 4 + g], Xb = xsum4[(G0 + 2 * pp + 1) * 4 + g];
+          const uint32_t wd[4] = {sa.raw[pp].x, sa.raw[pp].y, sa.raw[pp].z, sa.raw[pp].w};
+          f32x4 ua = {0.f, 0.f, 0.f, 0.f}, ub = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // one MFMA per group of the pair: the lanes of the other group read zero tokens
+            const uint4 f = q4_frag(wd[j], q_mask, q_bias);
+            ua = mfma(xa_base[j][P * 16], f, ua);
+            ub = mfma(xb_base[j][P * 16], f, ub);
           }
-        } else {
-          const f32x4 accA = mfma(x1, a1, mfma(x0, a0, z));
-          f32x4 xg = z;
-          if (F::has_min) xg = mfma(x1, ones, mfma(x0, ones, z));
-          const float2 pa = F::scale_val(sa.sc[i]);
-          const float ca = pa.y - 128.f * pa.x;
+          const uint32_t sw[4] = {sa.sc.x, sa.sc.y, sa.sc.z, sa.sc.w};
+          const float2 pa = F::scale_val(sw[2 * pp]), pb = F::scale_val(sw[2 * pp + 1]);
+          const float ca = pa.y - 128.f * pa.x, cb = pb.y - 128.f * pb.x;
+          const float xa4[4] = {Xa.x, Xa.y, Xa.z, Xa.w}, xb4[4] = {Xb.x, Xb.y, Xb.z, Xb.w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            tA[r] = __builtin_fmaf(pa.x, accA[r], tA[r]);
-            if (F::has_min) tA[r] = __builtin_fmaf(ca, xg[r], tA[r]);
+            tA[r] = __builtin_fmaf(pa.x, ua[r], tA[r]);
+            tA[r] = __builtin_fmaf(ca, xa4[r], tA[r]);
+            tA[r] = __builtin_fmaf(pb.x, ub[r], tA[r]);
+            tA[r] = __builtin_fmaf(cb, xb4[r], tA[r]);
           }
-          if (MODE == 0) {
-            uint4 b0, b1;
-            F::convert(sbb.raw[i], b0, b1);
-            const f32x4 accB = mfma(x1, b1, mfma(x0, b0, z));
-            const float2 pb = F::scale_val(sbb.sc[i]);
-            const float cb = pb.y - 128.f * pb.x;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int G = G0 + i;
+          const uint4 x0 = xrow[(G * 8 + 2 * g) ^ c16], x1 = xrow[(G * 8 + 2 * g + 1) ^ c16];
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          uint4 a0, a1;
+          F::convert(sa.raw[i], a0, a1);
+          if (F::scale_group == 0) {
+            tA = mfma(x1, a1, mfma(x0, a0, tA));
+          } else {
+            const f32x4 accA = mfma(x1, a1, mfma(x0, a0, z));
+            f32x4 xg = z;
+            if (F::has_min) xg = mfma(x1, ones, mfma(x0, ones, z));
+            const float2 pa = F::scale_val(sa.sc[i]);
+            const float ca = pa.y - 128.f * pa.x;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              tB[r] = __builtin_fmaf(pb.x, accB[r], tB[r]);
-              if (F::has_min) tB[r] = __builtin_fmaf(cb, xg[r], tB[r]);
+              tA[r] = __builtin_fmaf(pa.x, accA[r], tA[r]);
+              if (F::has_min) tA[r] = __builtin_fmaf(ca, xg[r], tA[r]);
             }
           }
         }
       }
+      // the sums are materialised here, each step: otherwise the compiler sinks the scale
+      // loads and rescaling into the (conditional) stores at the end of the item, which
+      // costs one more memory round trip and keeps every group's raw sums live
+      asm volatile("" : "+v"(tA));
     };
-    Step<F> s0, s1, s0b, s1b;
-    load_step<F>(rowA, ws, nA, 0, g, K, s0);
-    if (MODE == 0) load_step<F>(rowB, ws, nB, 0, g, K, s0b);
-    for (int G0 = 0; G0 < NG; G0 += 8) {
-      load_step<F>(rowA, ws, nA, G0 + 4, g, K, s1);
-      if (MODE == 0) load_step<F>(rowB, ws, nB, G0 + 4, g, K, s1b);
-      compute(s0, s0b, G0);
-      if (G0 + 8 < NG) {
-        load_step<F>(rowA, ws, nA, G0 + 8, g, K, s0);
-        if (MODE == 0) load_step<F>(rowB, ws, nB, G0 + 8, g, K, s0b);
-      }
-      compute(s1, s1b, G0 + 4);
-    }
-    float rsA = 1.f, rsB = 1.f;
-    if (F::scale_group == 0) {
-      rsA = F::scale(ws, nA, 0, K).x;
-      if (MODE == 0) rsB = F::scale(ws, nB, 0, K).x;
-    }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = 4 * g + r;
-      if (tok >= ntok) break;
-      const size_t slot = off + t0 + tok;
-      if (MODE == 0) {
-        reinterpret_cast<uint16_t*>(out)[slot * (size_t)(N / 2) + r0 + c16] = to_bf16(silu(tA[r] * rsA) * (tB[r] * rsB));
+    for (int i = 0; i < NS; ++i) {
+      const int b = i % DEPTH;
+      compute(ring[b], i * 4);
+      if (i + DEPTH < NS) {
+        fetch(cur, i + DEPTH, ring[b]);
       } else {
-        reinterpret_cast<float*>(out)[slot * (size_t)N + r0 + c16] = tA[r] * rsA;
+        // the next item's tokens go out ahead of its first weight step: loads complete in
+        // order, so the token store at the boundary waits for them alone.  After the block's
+        // last item nxt is the first item again (loads no one uses): branch-free, so the
+        // load counter stays exact
+        if (i + DEPTH == NS) tt.load(X, nxt.row0, nxt.ntok);
+        fetch(nxt, i + DEPTH - NS, ring[b]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // per-row scale, then: down stores y; gate_up up waves leave u in LDS, gate waves keep g
+    {
+      const size_t n = row_of(cur);
+      const float rs = F::scale_group == 0 ? F::scale(cur.ws, n, 0, K).x : 1.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tA[r] *= rs;
+      if (MODE == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 4 * g + r;
+          if (tok >= cur.ntok) break;
+          reinterpret_cast<float*>(out)[(cur.row0 + tok) * (size_t)N + n] = tA[r];
+        }
+      } else if (up) {
+        ups[((k & 1) * WR + wt) * 64 + lane] = tA;
+      } else {
+        pend.t = tA, pend.row0 = cur.row0, pend.ntok = cur.ntok, pend.col = (int)n, pend.valid = true;
       }
     }
+    if (!nxt.valid) break;
+    // stage the next item's tokens into the other buffer (last read in item k - 1, which every
+    // wave finished before the previous boundary's barrier)
+    tt.store(xs + ((k + 1) & 1) * BUF, F::paired);
+    cur = nxt;
+    nxt = item_at(blockIdx.x + (k + 2) * gridDim.x);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (MODE == 0) {
+    lds_barrier();
+    if (!up && pend.valid) finish_gate(pend, k);  // the last item
   }
 }
 
@@ -431,6 +654,21 @@ __global__ void __launch_bounds__(PF_WPB * 64)
   }
 }
 
+// blocks of a kernel resident on the whole device at once (occupancy x CUs), per kernel
+inline int resident_blocks(const void* kern, int threads, size_t lds) {
+  static const void* keys[32];
+  static int vals[32], n = 0;
+  for (int i = 0; i < n; ++i)
+    if (keys[i] == kern) return vals[i];
+  int dev = 0, cus = 0, per = 0;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, lds);
+  const int v = (per > 0 ? per : 1) * (cus > 0 ? cus : 256);
+  if (n < 32) keys[n] = kern, vals[n] = v, ++n;
+  return v;
+}
+
 template <class F>
 void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const int* offsets, const int* counts,
                     void* out, int E, int N, int K, int mode, size_t eq, size_t es, int sb, int fixed_rows,
@@ -449,15 +687,13 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
                          eq, es, sb, fixed_rows, 1);
     return;
   }
-  // grouped experts: one expert per grid x, 16-row tiles / PF_WPB over y, token passes over z
-  const dim3 grid(E, (rows_out / 16 + PF_WPB - 1) / PF_WPB, PF_ZPASS);
-  const size_t lds = (size_t)PF_TOK * K * 2;
-  if (mode == 0)
-    hipLaunchKernelGGL((k_grouped<F, 0, 2048>), grid, dim3(PF_WPB * 64), lds, st, wq, ws, X, offsets, counts, out, N,
-                       eq, es, sb, fixed_rows);
-  else
-    hipLaunchKernelGGL((k_grouped<F, 1, 512>), grid, dim3(PF_WPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq,
-                       es, sb, fixed_rows);
+  // grouped experts: a persistent grid of as many blocks as are resident at once, walking the
+  // work items (expert, token pass, row block) the kernel derives from counts
+  const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
+                     (mode == 0 ? 2 * (PF_GWPB / 2) * 64 * 16 : 0) + (F::paired ? (size_t)K * 2 : 0);
+  auto kern = mode == 0 ? k_grouped<F, 0, 2048> : k_grouped<F, 1, 512>;
+  int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E);
 }
 
 // gate_up then down for all experts of a grouped batch

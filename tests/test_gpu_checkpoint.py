@@ -64,6 +64,12 @@ def test_checkpoint_prefill_chunked(tmp_path):
     rl = O.router_logits_rows(hn, L["router"], rows, E + 1, H)
     ri, rw, rs = O.moe_topk(rl, rows, E, 8, E + 1)
     ref = O.moe_prefill_layer(L, hn, rows, ri, rw, rs, x0, H, 512, 8)
-    # bf16 rounding of act may flip between GPU and oracle fp32 sums: a loose bound here, the
-    # flip-aware check of the same kernel chain is tests/test_gpu_prefill.py
-    assert_close(host(xa).reshape(rows, H), ref, rtol=5e-3, atol=5e-3, what="prefill vs oracle")
+    # bf16 rounding of act may flip between GPU and oracle fp32 sums, and a flip propagates
+    # through a whole down-projection column, so single elements can sit outside any fixed
+    # bound (the flip-aware check of the same kernel chain is tests/test_gpu_prefill.py).  Here
+    # the loader wiring is checked: a wrong tensor or argument breaks every row, so at most
+    # 1e-4 of the elements may exceed 5e-3 (abs + rel) and none may exceed 5e-2.
+    got = host(xa).reshape(rows, H).astype(np.float64)
+    err = np.abs(got - ref) - 5e-3 * (1 + np.abs(ref))
+    assert (err > 0).mean() <= 1e-4, f"prefill vs oracle: {int((err > 0).sum())} elements beyond 5e-3"
+    assert_close(got, ref, rtol=5e-2, atol=5e-2, what="prefill vs oracle")

@@ -119,25 +119,30 @@ __global__ void k_count(const int* __restrict__ idx, int n, int* __restrict__ co
 }
 
 // x[r, c] += sigmoid(sgate[r]) * shared[r, c] + sum_k wts[r, k] * y[slot_of[r, k], c], k ascending.
+// Block = one row and 1024 columns (one float4 per thread); TK > 0: topk fixed at compile time,
+// so all TK row loads of a thread are in flight together.
+template <int TK>
 __global__ void __launch_bounds__(256)
     k_combine(float* __restrict__ x, const float* __restrict__ y, const int* __restrict__ slot_of,
               const float* __restrict__ wts, const float* __restrict__ sgate, const float* __restrict__ shared,
               int topk, int H) {
-  const int r = blockIdx.x;
+  const int r = blockIdx.x, c = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (c >= H) return;
+  const int K = TK > 0 ? TK : topk;
   const float sg = sigmoid(sgate[r]);
-  for (int c = threadIdx.x * 4; c < H; c += blockDim.x * 4) {
-    const float4 sh = *reinterpret_cast<const float4*>(shared + (size_t)r * H + c);
-    float4 acc = make_float4(sg * sh.x, sg * sh.y, sg * sh.z, sg * sh.w);
-    for (int k = 0; k < topk; ++k) {
-      const float w = wts[r * topk + k];
-      const float4 v = *reinterpret_cast<const float4*>(y + (size_t)slot_of[r * topk + k] * H + c);
-      acc.x += w * v.x, acc.y += w * v.y, acc.z += w * v.z, acc.w += w * v.w;
-    }
-    float4* xo = reinterpret_cast<float4*>(x + (size_t)r * H + c);
-    float4 o = *xo;
-    o.x += acc.x, o.y += acc.y, o.z += acc.z, o.w += acc.w;
-    *xo = o;
+  const float4 sh = *reinterpret_cast<const float4*>(shared + (size_t)r * H + c);
+  float4 acc = make_float4(sg * sh.x, sg * sh.y, sg * sh.z, sg * sh.w);
+#pragma unroll
+  for (int k = 0; k < (TK > 0 ? TK : 32); ++k) {
+    if (TK == 0 && k >= K) break;
+    const float w = wts[r * K + k];
+    const float4 v = *reinterpret_cast<const float4*>(y + (size_t)slot_of[r * K + k] * H + c);
+    acc.x += w * v.x, acc.y += w * v.y, acc.z += w * v.z, acc.w += w * v.w;
   }
+  float4* xo = reinterpret_cast<float4*>(x + (size_t)r * H + c);
+  float4 o = *xo;
+  o.x += acc.x, o.y += acc.y, o.z += acc.z, o.w += acc.w;
+  *xo = o;
 }
 
 __global__ void k_dequant_q8(const int8_t* __restrict__ W, const uint16_t* __restrict__ S, uint16_t* __restrict__ out,
@@ -198,7 +203,11 @@ API int dr_moe_combine(float* x, const float* y, const int* slot_of, const float
                        const float* shared, int rows, int topk, int H, hipStream_t st) {
   if (topk < 1 || topk > 32 || H % 4 != 0) return -1;
   if (rows <= 0) return 0;
-  hipLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, x, y, slot_of, wts, sgate, shared, topk, H);
+  const dim3 grid(rows, (H / 4 + 255) / 256);
+  if (topk == 8)
+    hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, x, y, slot_of, wts, sgate, shared, topk, H);
+  else
+    hipLaunchKernelGGL(k_combine<0>, grid, dim3(256), 0, st, x, y, slot_of, wts, sgate, shared, topk, H);
   return 0;
 }
 

@@ -507,13 +507,13 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
 
 
 // K-split variant, used for the shared expert (one weight set over all rows; for the grouped
-// experts it measured slower than k_grouped).  Block = RT consecutive 16-row tiles of weight rows (gate_up: 16 gate +
-// 16 up rows per tile) of one expert; wave w owns the input groups [GPW w, GPW (w + 1)) of
-// every row, so each wave issues all loads of a tile at once, and the next tile's weights
-// stream in while the current one is used.  Per row tile the weights stay in registers for
-// every 16-token tile of the expert (tiles blockIdx.z, + gridDim.z, ...); a wave reads its
-// slice of the 16 tokens straight from global memory (no LDS staging), runs the exact-dequant
-// MFMA steps, and the eight partial 16 x 16 tiles are summed through LDS in wave order.
+// experts it measured slower than k_grouped).  Block = one 16-row tile of weight rows (gate_up:
+// 16 gate + 16 up rows) of one expert; wave w owns the input groups [GPW w, GPW (w + 1)) of
+// every row, so each wave issues all loads of the tile at once.  The weights stay in registers
+// for every 16-token tile of the expert (tiles blockIdx.z, + gridDim.z, ...); a wave reads its
+// slice of the 16 tokens straight from global memory (no LDS staging; the next tile's slice is
+// loaded while the current one is used), runs the exact-dequant MFMA steps, and the eight
+// partial 16 x 16 tiles are summed through LDS in wave order.
 template <class F>
 struct Wts {
   typename Raw<F>::T a, b;
@@ -540,7 +540,7 @@ template <class F, int MODE, int K>
 __global__ void __launch_bounds__(PF_WPB * 64)
     k_grouped_ks(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
                  const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
-                 size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int fixed_rows, int RT) {
+                 size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int fixed_rows) {
   constexpr int NG = K / 64, GPW = NG / PF_WPB;
   static_assert(GPW * PF_WPB == NG, "groups per wave");
   __shared__ float red[PF_WPB][8][64];
@@ -558,29 +558,43 @@ __global__ void __launch_bounds__(PF_WPB * 64)
   const int G0 = wave * GPW;
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  Wts<F> cur[GPW], nxt[GPW];
-  load_tile<F, MODE, K>(wq, ws, rb, half, blockIdx.y * RT * 16, G0, g, c16, cur);
-  for (int t = 0; t < RT; ++t) {
-    const int r0 = (blockIdx.y * RT + t) * 16;
-    // the next row tile (the last one reloads itself: a conditional load would make the
-    // compiler wait for every outstanding load before using the current tile)
-    load_tile<F, MODE, K>(wq, ws, rb, half, (blockIdx.y * RT + (t + 1 < RT ? t + 1 : t)) * 16, G0, g, c16, nxt);
-    for (int tile = blockIdx.z; tile < tiles; tile += gridDim.z) {
-      // this lane's token row (MFMA A row c16), its 16 inputs 64 G + 16 g .. + 15 per group
+  Wts<F> cur[GPW];
+  load_tile<F, MODE, K>(wq, ws, rb, half, blockIdx.y * 16, G0, g, c16, cur);
+  {
+    const int r0 = blockIdx.y * 16;
+    // this lane's token row (MFMA A row c16) of a tile, its 16 inputs 64 G + 16 g .. + 15 per
+    // group; the next tile's rows are loaded before the current one is used (rows past the
+    // end load the last row and are zeroed: straight-line code keeps the load counter exact)
+    auto load_x = [&](int tile, uint4 (&x0)[GPW], uint4 (&x1)[GPW]) {
       const int tok = tile * PF_TOK + c16;
       const uint16_t* xr = X + (off + (size_t)(tok < cnt ? tok : cnt - 1)) * K;
-      uint4 x0[GPW], x1[GPW];
 #pragma unroll
       for (int i = 0; i < GPW; ++i) {
         const int k0 = 64 * (G0 + i) + 16 * g;
-        uint4 v0 = ld16(xr + k0), v1 = ld16(xr + k0 + 8);
-        if (tok >= cnt) v0 = v1 = make_uint4(0, 0, 0, 0);
+        x0[i] = ld16(xr + k0), x1[i] = ld16(xr + k0 + 8);
+      }
+    };
+    auto perm_x = [&](int tile, uint4 (&x0)[GPW], uint4 (&x1)[GPW]) {
+      const bool live = tile * PF_TOK + c16 < cnt;
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) {
+        const uint4 v0 = live ? x0[i] : make_uint4(0, 0, 0, 0), v1 = live ? x1[i] : make_uint4(0, 0, 0, 0);
         // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7)
         x0[i] = make_uint4(__builtin_amdgcn_perm(v0.z, v0.x, 0x05040100u), __builtin_amdgcn_perm(v0.z, v0.x, 0x07060302u),
                            __builtin_amdgcn_perm(v0.w, v0.y, 0x05040100u), __builtin_amdgcn_perm(v0.w, v0.y, 0x07060302u));
         x1[i] = make_uint4(__builtin_amdgcn_perm(v1.z, v1.x, 0x05040100u), __builtin_amdgcn_perm(v1.z, v1.x, 0x07060302u),
                            __builtin_amdgcn_perm(v1.w, v1.y, 0x05040100u), __builtin_amdgcn_perm(v1.w, v1.y, 0x07060302u));
       }
+    };
+    uint4 nx0[GPW], nx1[GPW];
+    load_x(blockIdx.z, nx0, nx1);
+    for (int tile = blockIdx.z; tile < tiles; tile += gridDim.z) {
+      uint4 x0[GPW], x1[GPW];
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) x0[i] = nx0[i], x1[i] = nx1[i];
+      const int nt = tile + gridDim.z;
+      load_x(nt < tiles ? nt : tile, nx0, nx1);
+      perm_x(tile, x0, x1);
       f32x4 tA = z, tB = z;
 #pragma unroll
       for (int i = 0; i < GPW; ++i) {
@@ -649,8 +663,6 @@ __global__ void __launch_bounds__(PF_WPB * 64)
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < GPW; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -681,10 +693,10 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
     const dim3 grid(1, rows_out / 16, tiles < 8 ? tiles : 8);
     if (mode == 0)
       hipLaunchKernelGGL((k_grouped_ks<F, 0, 2048>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out,
-                         N, eq, es, sb, fixed_rows, 1);
+                         N, eq, es, sb, fixed_rows);
     else
       hipLaunchKernelGGL((k_grouped_ks<F, 1, 512>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out, N,
-                         eq, es, sb, fixed_rows, 1);
+                         eq, es, sb, fixed_rows);
     return;
   }
   // grouped experts: a persistent grid of as many blocks as are resident at once, walking the

@@ -400,11 +400,24 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     f32x4 tA = {0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const Step<F>& sa, int G0) {
       if constexpr (F::paired) {
-        const float4* xsum4 = reinterpret_cast<const float4*>(xb + PF_TOK * K / 8);
+        // min term of the step's four groups as one fp32 MFMA: A = group sums X[token c16][G0 + g],
+        // B = (m - 128 s)[row c16][G0 + g] (this lane's scale word g)
+        {
+          const float xg = reinterpret_cast<const float*>(xb + PF_TOK * K / 8)[(G0 + g) * 16 + c16];
+          // (selecting among decoded floats: a select among the step's words becomes an indexed
+          // access that sends the whole ring to scratch memory)
+          const float2 p0 = F::scale_val(sa.sc.x), p1 = F::scale_val(sa.sc.y);
+          const float2 p2 = F::scale_val(sa.sc.z), p3 = F::scale_val(sa.sc.w);
+          const float c0 = p0.y - 128.f * p0.x, c1 = p1.y - 128.f * p1.x;
+          const float c2 = p2.y - 128.f * p2.x, c3 = p3.y - 128.f * p3.x;
+          const float cg = g & 2 ? (g & 1 ? c3 : c2) : (g & 1 ? c1 : c0);
+          // accumulated straight into tA, step by step: the min terms cancel most of the 128 q
+          // offset of the products, and summing them apart would lose that cancellation's bits
+          tA = __builtin_amdgcn_mfma_f32_16x16x4f32(xg, cg, tA, 0, 0, 0);
+        }
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
           const int P = G0 / 2 + pp;
-          const float4 Xa = xsum4[(G0 + 2 * pp) * 4 + g], Xb = xsum4[(G0 + 2 * pp + 1) * 4 + g];
           const uint32_t wd[4] = {sa.raw[pp].x, sa.raw[pp].y, sa.raw[pp].z, sa.raw[pp].w};
           f32x4 ua = {0.f, 0.f, 0.f, 0.f}, ub = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -415,15 +428,11 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
             ub = mfma(xb_base[j][P * 16], f, ub);
           }
           const uint32_t sw[4] = {sa.sc.x, sa.sc.y, sa.sc.z, sa.sc.w};
-          const float2 pa = F::scale_val(sw[2 * pp]), pb = F::scale_val(sw[2 * pp + 1]);
-          const float ca = pa.y - 128.f * pa.x, cb = pb.y - 128.f * pb.x;
-          const float xa4[4] = {Xa.x, Xa.y, Xa.z, Xa.w}, xb4[4] = {Xb.x, Xb.y, Xb.z, Xb.w};
+          const float sca = F::scale_val(sw[2 * pp]).x, scb = F::scale_val(sw[2 * pp + 1]).x;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            tA[r] = __builtin_fmaf(pa.x, ua[r], tA[r]);
-            tA[r] = __builtin_fmaf(ca, xa4[r], tA[r]);
-            tA[r] = __builtin_fmaf(pb.x, ub[r], tA[r]);
-            tA[r] = __builtin_fmaf(cb, xb4[r], tA[r]);
+            tA[r] = __builtin_fmaf(sca, ua[r], tA[r]);
+            tA[r] = __builtin_fmaf(scb, ub[r], tA[r]);
           }
         }
       } else {

@@ -34,6 +34,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int PF_WPB = 8;     // waves per block (k_grouped_ks)
 constexpr int PF_GWPB = 8;    // waves per block (k_grouped)
+constexpr int PF_GRPW = 2;    // 16-row tiles per wave and item (k_grouped): one token tile serves both
 constexpr int PF_TOK = 16;    // tokens per pass (one MFMA tile)
 constexpr int PF_MAXE = 256;  // experts
 constexpr int PF_DEPTH = 4;   // 4-group weight steps in flight per wave (k_grouped)
@@ -157,13 +158,16 @@ struct TokTile {
   static constexpr int NB = PF_TOK * K / 8 / NT;  // 16-byte blocks per thread (NT threads)
   static_assert(NB >= 1 && NB * NT == PF_TOK * K / 8, "token tile split");
   uint4 v[NB];
+  // rows [row0, row0 + ntok) through a buffer resource bounded at the last row: the lanes of
+  // rows past ntok read zeros without a memory access (and the code stays branch-free, which
+  // keeps the load counter exact)
   DEV void load(const uint16_t* __restrict__ X, size_t row0, int ntok) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(X + row0 * (size_t)K), 0, ntok * K * 2, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int b = threadIdx.x + i * NT, t = b / (K / 8), r = b % (K / 8);
-      // rows past ntok load row0 again (straight-line code keeps the load counter exact) and are zeroed
-      const uint4 w = ld16(X + (row0 + (t < ntok ? t : 0)) * (size_t)K + r * 8);
-      v[i] = t < ntok ? w : make_uint4(0, 0, 0, 0);
+      v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (t * K + r * 8) * 2, 0, 0));
     }
   }
   // with_sums: also the fp32 sum of every 64-input group of every token, at float index
@@ -253,12 +257,12 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   constexpr int WR = MODE == 0 ? PF_GWPB / 2 : PF_GWPB;  // row tiles per item (per row set)
   const int lane = lane_id(), wave = wave_id();
   const int g = lane >> 4, c16 = lane & 15;
-  const int YB = (MODE == 0 ? N / 2 : N) / (16 * WR);  // row blocks per expert
+  const int YB = (MODE == 0 ? N / 2 : N) / (16 * WR * PF_GRPW);  // row blocks per expert
   // per lane: pass counts of experts 4 lane + j and their inclusive prefix over all experts;
   // (end of passes, count, offset) of each kept in LDS; every wave writes the same values and
   // each lane reads back only its own entries, so no barrier is needed
   uint4* tbl = xs + 2 * BUF;
-  f32x4* ups = reinterpret_cast<f32x4*>(tbl + 192);  // [2][WR][64] up results (gate_up)
+  f32x4* ups = reinterpret_cast<f32x4*>(tbl + 192);  // [2][PF_GRPW][WR][64] up results (gate_up)
   int n_pass;
   {
     int cl[4], ol[4], pl[4], psum = 0;
@@ -325,16 +329,19 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     return it;
   };
   const size_t rb = F::row_bytes(K);
-  constexpr int NS = K / 256;  // 4-group steps per item
+  constexpr int SPT = K / 256;         // 4-group steps per tile
+  constexpr int NS = PF_GRPW * SPT;    // per item
   constexpr int DEPTH = PF_DEPTH < NS ? PF_DEPTH : NS;
   static_assert(NS % DEPTH == 0, "the ring of steps must divide an item");
   const bool up = MODE == 0 && wave >= WR;  // gate_up: this wave computes up rows
   const int wt = wave % WR;
   // weight row of this lane in item it (gate_up: the up row of an up wave)
-  auto row_of = [&](const Item& it) { return (size_t)(up ? N / 2 : 0) + (size_t)((it.yb * WR + wt) * 16 + c16); };
+  auto row_of = [&](const Item& it, int t) {
+    return (size_t)(up ? N / 2 : 0) + (size_t)(((it.yb * PF_GRPW + t) * WR + wt) * 16 + c16);
+  };
   auto fetch = [&](const Item& it, int s, Step<F>& st) {
-    const size_t n = row_of(it);
-    load_step<F>(it.wq + n * rb, it.ws, n, s * 4, g, K, st);
+    const size_t n = row_of(it, s / SPT);
+    load_step<F>(it.wq + n * rb, it.ws, n, (s % SPT) * 4, g, K, st);
   };
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
   // the int4 conversion constants live in VGPRs: v_and_or_b32 (VOP3) takes no literal
@@ -344,7 +351,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   asm volatile("" : "+v"(q_mask), "+v"(q_bias));
   // zero tokens for the int4 pair MFMAs (K / 8 blocks: every offset a pair's read adds stays
   // inside); each wave writes the whole block itself before its own reads, so no barrier
-  const uint4* zeros = reinterpret_cast<const uint4*>(ups + (MODE == 0 ? 2 * WR * 64 : 0));
+  const uint4* zeros = reinterpret_cast<const uint4*>(ups + (MODE == 0 ? 2 * PF_GRPW * WR * 64 : 0));
   if (F::paired) {
     uint4* z = const_cast<uint4*>(zeros);
     for (int i = lane; i < K / 8; i += 64) z[i] = make_uint4(0, 0, 0, 0);
@@ -367,19 +374,23 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   // gate_up: the gate waves finish item k - 1 after the boundary barrier, with the up results
   // the up waves left in ups[(k - 1) & 1]
   struct Pending {
-    f32x4 t;
+    f32x4 t[PF_GRPW];
     size_t row0;
-    int ntok, col;
+    int ntok, col[PF_GRPW];
     bool valid;
   } pend;
   pend.valid = false;
   auto finish_gate = [&](const Pending& pd, int k1) {
-    const f32x4 u = ups[((k1 & 1) * WR + wt) * 64 + lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = 4 * g + r;
-      if (tok >= pd.ntok) break;
-      reinterpret_cast<uint16_t*>(out)[(pd.row0 + tok) * (size_t)(N / 2) + pd.col] = to_bf16(silu(pd.t[r]) * u[r]);
+    for (int t = 0; t < PF_GRPW; ++t) {
+      const f32x4 u = ups[(((k1 & 1) * PF_GRPW + t) * WR + wt) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 4 * g + r;
+        if (tok >= pd.ntok) break;
+        reinterpret_cast<uint16_t*>(out)[(pd.row0 + tok) * (size_t)(N / 2) + pd.col[t]] =
+            to_bf16(silu(pd.t[t][r]) * u[r]);
+      }
     }
   };
   int k = 0;
@@ -467,7 +478,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int b = i % DEPTH;
-      compute(ring[b], i * 4);
+      compute(ring[b], (i % SPT) * 4);
       if (i + DEPTH < NS) {
         fetch(cur, i + DEPTH, ring[b]);
       } else {
@@ -479,10 +490,11 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
         fetch(nxt, i + DEPTH - NS, ring[b]);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    // per-row scale, then: down stores y; gate_up up waves leave u in LDS, gate waves keep g
-    {
-      const size_t n = row_of(cur);
+      if ((i + 1) % SPT != 0) continue;
+      // end of tile t: per-row scale, then down stores y; gate_up up waves leave u in LDS,
+      // gate waves keep g until the boundary
+      const int t = i / SPT;
+      const size_t n = row_of(cur, t);
       const float rs = F::scale_group == 0 ? F::scale(cur.ws, n, 0, K).x : 1.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) tA[r] *= rs;
@@ -494,10 +506,12 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
           reinterpret_cast<float*>(out)[(cur.row0 + tok) * (size_t)N + n] = tA[r];
         }
       } else if (up) {
-        ups[((k & 1) * WR + wt) * 64 + lane] = tA;
+        ups[(((k & 1) * PF_GRPW + t) * WR + wt) * 64 + lane] = tA;
       } else {
-        pend.t = tA, pend.row0 = cur.row0, pend.ntok = cur.ntok, pend.col = (int)n, pend.valid = true;
+        pend.t[t] = tA, pend.col[t] = (int)n;
+        pend.row0 = cur.row0, pend.ntok = cur.ntok, pend.valid = true;
       }
+      tA = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     if (!nxt.valid) break;
     // stage the next item's tokens into the other buffer (last read in item k - 1, which every
@@ -711,7 +725,7 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
   // grouped experts: a persistent grid of as many blocks as are resident at once, walking the
   // work items (expert, token pass, row block) the kernel derives from counts
   const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
-                     (mode == 0 ? 2 * (PF_GWPB / 2) * 64 * 16 : 0) + (F::paired ? (size_t)K * 2 : 0);
+                     (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0) + (F::paired ? (size_t)K * 2 : 0);
   auto kern = mode == 0 ? k_grouped<F, 0, 2048> : k_grouped<F, 1, 512>;
   int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E);

@@ -338,9 +338,21 @@ def main():
                 _, xs = O.moe_decode(hl, xs, ri, rw, rs, xs, H, I, TOPK, nw=h["nw"], eps=1e-6)
                 t_cpu += time.perf_counter() - t1
                 n += 1
+            # the same layer on one thread (a shorter sample), for the per-core figure
+            O.lib().or_set_threads(1)
+            n1, t1s = 0, 0.0
+            while t1s < args.cpu_seconds / 3 and n1 < 2000:
+                t1 = time.perf_counter()
+                _, ri, rw, rs = O.router_topk(h["router"].view(np.uint16), xs, h["nw"], 1e-6, E, TOPK)
+                _, xs = O.moe_decode(hl, xs, ri, rw, rs, xs, H, I, TOPK, nw=h["nw"], eps=1e-6)
+                t1s += time.perf_counter() - t1
+                n1 += 1
+            O.lib().or_set_threads(threads)
             cpu = {"value": round(t_cpu / n * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
                    "sample": f"{n} decode layers (router + 8 int4 experts + int8 shared, fp64 accumulation) of layer 0, "
-                             f"{t_cpu:.1f} s"}
+                             f"{t_cpu:.1f} s",
+                   "value_1thread": round(t1s / n1 * 1e6, 1),
+                   "sample_1thread": f"{n1} decode layers on 1 thread, {t1s:.1f} s"}
         except Exception as e:
             cpu = {"error": repr(e)}
 

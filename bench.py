@@ -312,7 +312,23 @@ def main():
         import benchcfg
 
         extra = {}
-        for name, fn in (("cfg1_gemv_int4", lambda: benchcfg.config1_gemv(lib, st)),
+
+        def config2_single_layer(iters=200):
+            # one decode layer per call (the fused step over one layer, and the per-layer chain),
+            # rotating over the resident layers so that no call finds its weights in the MALL
+            def fused_one(i):
+                rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * (i % nl), 1, P(x), E, H, I, TOPK, 1e-6, P(ll),
+                                                  P(sync), None, None, None, None, sp)
+                assert rc == 0
+            out = {}
+            for key, fn in (("fused_one_layer", fused_one), ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
+                ms = benchcfg.timed(fn, iters, st)
+                out[key] = benchcfg.rec(ms * 1000, bytes_step // nl)
+            out["note"] = "one launch (fused) or three launches (chain) per layer, launch latency included"
+            return out
+
+        for name, fn in (("cfg2_one_layer", config2_single_layer),
+                         ("cfg1_gemv_int4", lambda: benchcfg.config1_gemv(lib, st)),
                          ("cfg4_prefill_int4", lambda: benchcfg.config4_prefill(lib, layers, st)),
                          ("cfg5_fp8_and_int8", lambda: benchcfg.config5_fp8(lib, st))):
             try:

@@ -49,6 +49,7 @@ DEV f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
 // int4, (scale, min) pairs per 64 inputs; SC = ScaleF16 | ScaleBF16
 template <class SC>
 struct FmtQ4 {
+  static constexpr bool q8 = false;
   static constexpr bool has_min = true;
   static constexpr bool paired = true;  // k_grouped: 16-byte loads covering two groups per row
   static constexpr int scale_group = 64;  // inputs per scale
@@ -72,6 +73,8 @@ struct FmtQ4 {
 // int8: 16 bytes per lane and group; bytes k..k+15 of the group slice, reordered
 template <class SH>
 struct FmtQ8 {
+  using Scale = SH;
+  static constexpr bool q8 = true;
   static constexpr bool has_min = false;
   static constexpr bool paired = false;
   static constexpr int scale_group = SH::per_row ? 0 : 128;
@@ -99,6 +102,7 @@ struct FmtQ8 {
 // fp8 e4m3 (OCP), one scale per 128 x 128 block; SF: 0 = f32 scales, 1 = bf16 scales
 template <int SF>
 struct FmtFP8 {
+  static constexpr bool q8 = false;
   static constexpr bool has_min = false;
   static constexpr bool paired = false;
   static constexpr int scale_group = 128;
@@ -689,6 +693,111 @@ __global__ void __launch_bounds__(PF_WPB * 64)
   }
 }
 
+// Shared-expert down projection over all prefill rows (one int8 weight set, dense, y = D act):
+// a weight-stationary MFMA GEMM.  Block = 4 waves, 32 token rows x 32 weight rows.  The block's 32 rows (all K) are staged once in LDS
+// (padded rows), then wave w streams half the inputs (K half w / 2) of the 16 token rows
+// 16 (w % 2) .. of the block straight from global memory, DQ_D 64-input groups ahead, against
+// both 16-row weight tiles (no barrier in the K loop); the two halves are summed through LDS.  Exact dequant as in k_grouped (int8 -> bf16 exactly; scale per row at the end,
+// or per 128 inputs for the reference layout).
+constexpr int DQ_TM = 32, DQ_D = 8;
+
+template <class SH, int K>
+__global__ void __launch_bounds__(256)
+    k_dense_q8(const uint8_t* __restrict__ Wq, const uint16_t* __restrict__ Ws, const uint16_t* __restrict__ X,
+               float* __restrict__ out, int rows, int N) {
+  using F = FmtQ8<SH>;
+  constexpr int WROW = K + 16, NG = K / 64, NW = 32 * K / 16 / 256;  // LDS row bytes, groups, fill loads
+  constexpr int NH = NG / 2;  // groups per K half
+  constexpr int D = DQ_D < NH ? DQ_D : NH;  // groups in flight
+  static_assert(NH % D == 0 && NW >= 1, "shape");
+  extern __shared__ uint4 dq_lds[];
+  uint8_t* wl = reinterpret_cast<uint8_t*>(dq_lds);
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int g = lane >> 4, c16 = lane & 15;
+  const int t0 = blockIdx.x * DQ_TM;
+  auto wrow = [&](int i) { return (size_t)(blockIdx.y * 32 + i); };
+  // this lane's token row (MFMA A row c16 of wave w's tile), read through a buffer resource
+  // bounded at the last row: rows past it read zeros without a fetch
+  const int ntok = min(DQ_TM, rows - t0);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(X + (size_t)t0 * K), 0, ntok * K * 2, 0x00020000);
+  const int tok = (wave & 1) * 16 + c16, kh = wave >> 1;
+  auto xload = [&](int G, uint4& v0, uint4& v1) {
+    const int off = (tok * K + 64 * G + 16 * g) * 2;
+    v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+  };
+  // weights: NW 16-byte pieces per thread, all loads first, then the LDS stores
+  {
+    uint4 wv[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int p = tid + 256 * q, r = p / (K / 16), b = p % (K / 16);
+      wv[q] = ld16(Wq + wrow(r) * (size_t)K + b * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int p = tid + 256 * q, r = p / (K / 16), b = p % (K / 16);
+      *reinterpret_cast<uint4*>(wl + r * WROW + b * 16) = wv[q];
+    }
+  }
+  uint4 xa[D], xb[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) xload(kh * NH + d, xa[d], xb[d]);
+  __syncthreads();
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 tA = z, tB = z, cA = z, cB = z;
+#pragma unroll 1
+  for (int G0 = kh * NH; G0 < (kh + 1) * NH; G0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int G = G0 + d;
+      // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e4)(e1 e5)(e2 e6)(e3 e7): the fragment order of FmtQ8
+      const uint4 v0 = xa[d], v1 = xb[d];
+      const uint4 x0 = make_uint4(__builtin_amdgcn_perm(v0.z, v0.x, 0x05040100u), __builtin_amdgcn_perm(v0.z, v0.x, 0x07060302u),
+                                  __builtin_amdgcn_perm(v0.w, v0.y, 0x05040100u), __builtin_amdgcn_perm(v0.w, v0.y, 0x07060302u));
+      const uint4 x1 = make_uint4(__builtin_amdgcn_perm(v1.z, v1.x, 0x05040100u), __builtin_amdgcn_perm(v1.z, v1.x, 0x07060302u),
+                                  __builtin_amdgcn_perm(v1.w, v1.y, 0x05040100u), __builtin_amdgcn_perm(v1.w, v1.y, 0x07060302u));
+      if (G + D < (kh + 1) * NH) xload(G + D, xa[d], xb[d]);
+      uint4 a0, a1, b0, b1;
+      F::convert(*reinterpret_cast<const uint4*>(wl + c16 * WROW + G * 64 + g * 16), a0, a1);
+      F::convert(*reinterpret_cast<const uint4*>(wl + (16 + c16) * WROW + G * 64 + g * 16), b0, b1);
+      cA = mfma(x1, a1, mfma(x0, a0, cA));
+      cB = mfma(x1, b1, mfma(x0, b0, cB));
+      if (!SH::per_row && (G & 1)) {
+        // per 128 inputs: scale the pair of groups, restart
+        const float sa = SH::scale(Ws, wrow(c16), G * 64, K), sb = SH::scale(Ws, wrow(16 + c16), G * 64, K);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tA[r] = __builtin_fmaf(sa, cA[r], tA[r]), tB[r] = __builtin_fmaf(sb, cB[r], tB[r]);
+        cA = z, cB = z;
+      }
+    }
+  }
+  float sa = 1.f, sb = 1.f;
+  if (SH::per_row) {
+    tA = cA, tB = cB;
+    sa = SH::scale(Ws, wrow(c16), 0, K), sb = SH::scale(Ws, wrow(16 + c16), 0, K);
+  }
+  // the upper K half hands its sums to the lower one (LDS after the weights)
+  f32x4* red = reinterpret_cast<f32x4*>(wl + 32 * WROW);
+  if (kh == 1) red[((wave & 1) * 2) * 64 + lane] = tA, red[((wave & 1) * 2 + 1) * 64 + lane] = tB;
+  __syncthreads();
+  if (kh == 1) return;
+  {
+    const f32x4 ua = red[((wave & 1) * 2) * 64 + lane], ub = red[((wave & 1) * 2 + 1) * 64 + lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tA[r] += ua[r], tB[r] += ub[r];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = (wave & 1) * 16 + 4 * g + r;
+    if (t >= ntok) break;
+    float* y = out + (size_t)(t0 + t) * N + blockIdx.y * 32;
+    y[c16] = tA[r] * sa;
+    y[16 + c16] = tB[r] * sb;
+  }
+}
+
 // blocks of a kernel resident on the whole device at once (occupancy x CUs), per kernel
 inline int resident_blocks(const void* kern, int threads, size_t lds) {
   static const void* keys[32];
@@ -710,16 +819,19 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
                     hipStream_t st) {
   const int rows_out = mode == 0 ? N / 2 : N;
   if (fixed_rows >= 0) {
-    // one weight set over all rows (the shared expert): the K-split kernel, one 16-row tile
-    // per block, token tiles over grid z (measured 2x faster than k_grouped here)
-    const int tiles = (fixed_rows + PF_TOK - 1) / PF_TOK;
-    const dim3 grid(1, rows_out / 16, tiles < 8 ? tiles : 8);  // z = 4, 16, 32 measured slower
-    if (mode == 0)
+    // one weight set over all rows (the shared expert).  gate_up: the K-split kernel, one
+    // 16-row tile per block, token tiles over grid z (z = 4, 16, 32 and the dense kernel measured
+    // slower); down: the dense weight-stationary kernel (6.6 against 10.2 us at 300 rows)
+    if (mode == 0) {
+      const int tiles = (fixed_rows + PF_TOK - 1) / PF_TOK;
+      const dim3 grid(1, rows_out / 16, tiles < 8 ? tiles : 8);
       hipLaunchKernelGGL((k_grouped_ks<F, 0, 2048>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out,
                          N, eq, es, sb, fixed_rows);
-    else
-      hipLaunchKernelGGL((k_grouped_ks<F, 1, 512>), grid, dim3(PF_WPB * 64), 0, st, wq, ws, X, offsets, counts, out, N,
-                         eq, es, sb, fixed_rows);
+    } else if constexpr (F::q8) {  // fixed_rows is the int8 shared expert's mode only
+      const dim3 grid((fixed_rows + DQ_TM - 1) / DQ_TM, N / 32);
+      hipLaunchKernelGGL((k_dense_q8<typename F::Scale, 512>), grid, dim3(256), 32 * (512 + 16) + 4096, st, wq,
+                         reinterpret_cast<const uint16_t*>(ws), X, reinterpret_cast<float*>(out), fixed_rows, N);
+    }
     return;
   }
   // grouped experts: a persistent grid of as many blocks as are resident at once, walking the

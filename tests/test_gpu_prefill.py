@@ -162,7 +162,7 @@ def test_grouped_gemm(fmt, kind, skew):
 
 
 @pytest.mark.parametrize("fmt", ["cfg", "ref"])
-@pytest.mark.parametrize("rows", [300, 5])
+@pytest.mark.parametrize("rows", [300, 33, 5, 1])
 def test_shared_prefill(fmt, rows):
     import torch
 

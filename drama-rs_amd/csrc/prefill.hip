@@ -23,6 +23,8 @@
 // token tile in LDS is stored in the same permuted order, 16-byte chunk b of token t at
 // b ^ (t % 16) so the 16 token rows of one read spread over all banks; each A fragment is one
 // 16-byte LDS read.  Weight loads run two steps ahead of the MFMAs.
+#include <mutex>
+
 #include "common.hpp"
 
 using namespace drm;
@@ -798,18 +800,22 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// blocks of a kernel resident on the whole device at once (occupancy x CUs), per kernel
+// blocks of a kernel resident on the whole current device at once (occupancy x CUs), cached
+// per (kernel, device); launchers may be called from several host threads
 inline int resident_blocks(const void* kern, int threads, size_t lds) {
-  static const void* keys[32];
-  static int vals[32], n = 0;
-  for (int i = 0; i < n; ++i)
-    if (keys[i] == kern) return vals[i];
-  int dev = 0, cus = 0, per = 0;
+  static std::mutex mu;
+  static const void* keys[64];
+  static int devs[64], vals[64], n = 0;
+  int dev = 0;
   (void)hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n; ++i)
+    if (keys[i] == kern && devs[i] == dev) return vals[i];
+  int cus = 0, per = 0;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, lds);
   const int v = (per > 0 ? per : 1) * (cus > 0 ? cus : 256);
-  if (n < 32) keys[n] = kern, vals[n] = v, ++n;
+  if (n < 64) keys[n] = kern, devs[n] = dev, vals[n] = v, ++n;
   return v;
 }
 

@@ -27,6 +27,8 @@
 //
 // Every wait is bounded: after ~0.2 s without progress the block writes sync[1] = 1 and
 // returns, and a launch that finds sync[1] != 0 returns at once, so the grid always drains.
+#include <atomic>
+
 #include "canon.hpp"
 #include "drama_moe.h"
 
@@ -491,16 +493,16 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
 // The grid needs all ST_NB workgroups resident at once; checked once per device.
 int step_grid_ok(const void* kernel) {
-  static int ok[64] = {0};  // 0 unknown, 1 yes, -1 no
+  static std::atomic<int> ok[64];  // 0 unknown, 1 yes, -1 no (launchers may run on several threads)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (ok[dev] == 0) {
+  if (ok[dev].load(std::memory_order_relaxed) == 0) {
     int cus = 0, per = 0;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, ST_NT, 0);
-    ok[dev] = (cus * per >= ST_NB) ? 1 : -1;
+    ok[dev].store((cus * per >= ST_NB) ? 1 : -1, std::memory_order_relaxed);
   }
-  return ok[dev] == 1;
+  return ok[dev].load(std::memory_order_relaxed) == 1;
 }
 
 template <class SC, class SH>

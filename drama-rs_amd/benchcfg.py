@@ -181,15 +181,19 @@ def make_fp8_layer(seed):
     return L
 
 
-def config5_fp8(lib, st, iters=100):
+def config5_fp8(lib, st, iters=100, copies=4):
     out = {}
     L = make_fp8_layer(41)
+    # the calls rotate over `copies` copies of the layer at distinct addresses (3.2 GB), so no
+    # call finds its weights in the 256 MB MALL
+    Ls = [L] + [{k: v.clone() for k, v in L.items()} for _ in range(copies - 1)]
     sp, P = st.cuda_stream, D.ptr
     z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
     x = torch.randn(H, device="cuda")
     logits, idx, wts, sg, counter, act = z(E + 1), z(TOPK, torch.int32), z(TOPK), z(1), z(4, torch.int32), z(9 * I)
 
     def dec(i):
+        L = Ls[i % copies]
         lib.dr_router_topk(P(L["router"]), P(x), P(L["nw"]), 1e-6, P(logits), E, TOPK, H, P(idx), P(wts), P(sg),
                            P(counter), None, None, None, None, 0, 0, 0, 0, sp)
         lib.dr_moe_decode_fp8_bf16s(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]),
@@ -200,18 +204,18 @@ def config5_fp8(lib, st, iters=100):
     per_expert = sum(L[k].numel() * L[k].element_size() for k in ("gu_q", "gu_s", "d_q", "d_s")) // E
     shared = sum(L[k].numel() * L[k].element_size() for k in ("sgu_q", "sgu_s", "sd_q", "sd_s"))
     b1 = L["router"].numel() * 2 + TOPK * per_expert + shared + 6 * H * 4 + 2 * 9 * I * 4
-    out["decode_batch1"] = rec(ms * 1000, b1, note="router + fp8 gate_up + down + int8 shared; x evolves per call")
+    out["decode_batch1"] = rec(ms * 1000, b1, note="router + fp8 gate_up + down + int8 shared; x evolves per call; 4 layer copies rotated")
     # batch 4 through the grouped (prefill) path: union of up to 32 experts
     pf = Prefill(4, st)
 
     def b4(i):
-        pf.router(lib, L)
-        pf.experts(lib, L, fp8=True)
+        pf.router(lib, Ls[i % copies])
+        pf.experts(lib, Ls[i % copies], fp8=True)
 
     ms4 = timed(b4, iters, st)
     nb4, hit = pf.layer_bytes(L)
     out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, note="4 rows via the grouped MFMA path (bf16 act)")
-    del L
+    del L, Ls
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections
     g = torch.Generator(device="cuda").manual_seed(51)

@@ -36,7 +36,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int PF_WPB = 8;     // waves per block (k_grouped_ks)
 constexpr int PF_GWPB = 8;    // waves per block (k_grouped)
-constexpr int PF_GRPW = 2;    // 16-row tiles per wave and item (k_grouped): one token tile serves both
+// 16-row tiles per wave and item (k_grouped).  Measured: 2 (one token tile serving both) is
+// level with 1 at 300 prefill rows and 20% slower at 4 decode rows (fewer, larger items)
+constexpr int PF_GRPW = 1;
 constexpr int PF_TOK = 16;    // tokens per pass (one MFMA tile)
 constexpr int PF_MAXE = 256;  // experts
 constexpr int PF_DEPTH = 4;   // 4-group weight steps in flight per wave (k_grouped)

@@ -33,6 +33,33 @@ def timed(fn, iters, st, warmup=3):
     return a.elapsed_time(b) / iters  # ms
 
 
+def timed_graph(fn, iters, st, period):
+    """fn(0) .. fn(period - 1) captured once into a HIP graph (dr_graph_*), replayed: the
+    per-call time without host launch gaps, as a caller that records its step in a graph sees it."""
+    lib = D.lib()
+    sp = st.cuda_stream
+    torch.cuda.synchronize()
+    g = ctypes.c_void_p()
+    lib.dr_graph_begin(sp)
+    for i in range(period):
+        fn(i)
+    lib.dr_graph_end(sp, ctypes.byref(g))
+    try:
+        for _ in range(2):
+            lib.dr_graph_launch(g, sp)
+        st.synchronize()
+        reps = max(1, iters // period)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(reps):
+            lib.dr_graph_launch(g, sp)
+        b.record(st)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / (reps * period)  # ms
+    finally:
+        lib.dr_graph_destroy(g)
+
+
 def rec(us, nbytes, **kw):
     gbs = nbytes / (us * 1e-6) / 1e9
     out = {"us": round(us, 2), "bytes": int(nbytes), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM, 4)}
@@ -126,10 +153,13 @@ def config4_prefill(lib, layers, st, iters=40):
         pf.experts(lib, L)
 
     ms = timed(full, iters, st)
+    msg = timed_graph(full, iters, st, min(nl, 8))
     nbytes, hit = pf.layer_bytes(layers[0])
     cnt = pf.counts.cpu()
     uniform = rec(ms * 1000, nbytes, experts_hit=hit, rows_per_expert_max=int(cnt.max()), pairs=pf.n,
-                  note="router GEMM + top-k + shared + group + gather + grouped GEMM + combine")
+                  us_graph=round(msg * 1000, 2),
+                  note="router GEMM + top-k + shared + group + gather + grouped GEMM + combine; us_graph: replayed "
+                       "from a HIP graph")
     # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
     g = torch.Generator(device="cuda").manual_seed(31)
     hot = torch.randperm(E, generator=g, device="cuda")[: E // 10]
@@ -204,7 +234,10 @@ def config5_fp8(lib, st, iters=100, copies=4):
     per_expert = sum(L[k].numel() * L[k].element_size() for k in ("gu_q", "gu_s", "d_q", "d_s")) // E
     shared = sum(L[k].numel() * L[k].element_size() for k in ("sgu_q", "sgu_s", "sd_q", "sd_s"))
     b1 = L["router"].numel() * 2 + TOPK * per_expert + shared + 6 * H * 4 + 2 * 9 * I * 4
-    out["decode_batch1"] = rec(ms * 1000, b1, note="router + fp8 gate_up + down + int8 shared; x evolves per call; 4 layer copies rotated")
+    msg = timed_graph(dec, iters, st, copies)
+    out["decode_batch1"] = rec(ms * 1000, b1, us_graph=round(msg * 1000, 2),
+                               note="router + fp8 gate_up + down + int8 shared; x evolves per call; 4 layer copies "
+                                    "rotated; us_graph: the same calls replayed from a HIP graph")
     # batch 4 through the grouped (prefill) path: union of up to 32 experts
     pf = Prefill(4, st)
 
@@ -213,8 +246,10 @@ def config5_fp8(lib, st, iters=100, copies=4):
         pf.experts(lib, Ls[i % copies], fp8=True)
 
     ms4 = timed(b4, iters, st)
+    ms4g = timed_graph(b4, iters, st, copies)
     nb4, hit = pf.layer_bytes(L)
-    out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, note="4 rows via the grouped MFMA path (bf16 act)")
+    out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, us_graph=round(ms4g * 1000, 2),
+                               note="4 rows via the grouped MFMA path (bf16 act); us_graph: replayed from a HIP graph")
     del L, Ls
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections

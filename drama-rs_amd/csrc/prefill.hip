@@ -304,13 +304,30 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     int ntok, yb;
     bool valid;
   };
-  // item i: flat pass q = i % n_pass (consecutive blocks take consecutive experts), yb = i / n_pass
+  if (n_pass == 0) return;
+  // Item i -> (flat pass q, row block yb).  Blocks run on XCD blockIdx % 8, each XCD with its
+  // own L2: where the grid allows, the YB row blocks of a pass go to blocks of one XCD in the
+  // same round of gridDim.x items, so its token tile is fetched into that L2 once (round r,
+  // block b = x + 8 j: q = (8 r + x) EPR + j / YB, yb = j % YB with EPR passes per XCD and
+  // round).  Otherwise q = i % n_pass, yb = i / n_pass.  Indices past the last pass are
+  // invalid; they map to pass 0, row block 0 (loaded, never computed).
+  const int G = gridDim.x, EPR = (G / 8) / YB;
+  const bool xcd_map = G % 8 == 0 && EPR > 0 && (G / 8) % YB == 0;
   auto item_at = [&](int i) {
     Item it;
-    it.valid = i < n_items;
-    const int i0 = it.valid ? i : blockIdx.x;  // past the end: a valid item, never computed
-    const int q = i0 % n_pass;
-    it.yb = i0 / n_pass;
+    int q, yb;
+    if (xcd_map) {
+      const int rnd = i / G, b = i - rnd * G, j = b >> 3;
+      q = (rnd * 8 + (b & 7)) * EPR + j / YB;
+      yb = j % YB;
+      it.valid = q < n_pass;
+    } else {
+      it.valid = i < n_items;
+      q = i % n_pass;
+      yb = i / n_pass;
+    }
+    if (!it.valid) q = 0, yb = 0;
+    it.yb = yb;
     const uint4 en = tbl[lane], cn = tbl[64 + lane], of = tbl[128 + lane];
     const int ev[4] = {(int)en.x, (int)en.y, (int)en.z, (int)en.w}, cv[4] = {(int)cn.x, (int)cn.y, (int)cn.z, (int)cn.w};
     const int ov[4] = {(int)of.x, (int)of.y, (int)of.z, (int)of.w};

@@ -161,6 +161,18 @@ DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Spin until an LDS counter reaches target (acquire); bounded, so a broken protocol ends the
+// wait instead of hanging the GPU (the results are then wrong, which the tests catch).
+DEV void lds_wait_ge(const uint32_t* c, uint32_t target) {
+  for (int it = 0; it < (1 << 22); ++it) {
+    if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+DEV void lds_count(uint32_t* c) {
+  if (lane_id() == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 template <int K, int NT>
 struct TokTile {
   static constexpr int NB = PF_TOK * K / 8 / NT;  // 16-byte blocks per thread (NT threads)
@@ -387,6 +399,12 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   Item nxt = item_at(blockIdx.x + gridDim.x);
   Step<F> ring[DEPTH];  // steps in flight
   TokTile<K, PF_GWPB * 64> tt;
+  // Waves synchronise per item through LDS counters instead of a block barrier, so they may
+  // drift by up to half an item: n_stored = 8 (k + 1) once every wave stored its part of item
+  // k's tile; n_done = 8 (k + 1) once every wave finished computing item k; (gate_up) n_up /
+  // n_gate count the up results handed over and read, 4 per item.
+  __shared__ uint32_t n_stored, n_done, n_up, n_gate;
+  if (threadIdx.x == 0) n_stored = 0, n_done = 0, n_up = 0, n_gate = 0;
   {
     tt.load(X, cur.row0, cur.ntok);
 #pragma unroll
@@ -406,6 +424,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   } pend;
   pend.valid = false;
   auto finish_gate = [&](const Pending& pd, int k1) {
+    lds_wait_ge(&n_up, (uint32_t)(WR * (k1 + 1)));
 #pragma unroll
     for (int t = 0; t < PF_GRPW; ++t) {
       const f32x4 u = ups[(((k1 & 1) * PF_GRPW + t) * WR + wt) * 64 + lane];
@@ -417,6 +436,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
             to_bf16(silu(pd.t[t][r]) * u[r]);
       }
     }
+    lds_count(&n_gate);
   };
   int k = 0;
   for (;; ++k) {
@@ -504,17 +524,23 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     for (int i = 0; i < NS; ++i) {
       const int b = i % DEPTH;
       compute(ring[b], (i % SPT) * 4);
+      // the next item's tokens go out after step 0 (ahead of that step's weight fetch) and are
+      // stored into the other tile buffer at mid-item, once every wave finished item k - 1
+      // (the buffer's previous tile); after the block's last item nxt is the first item again
+      // (loads and stores no one uses): branch-free, so the load counter stays exact
+      if (i == 0) tt.load(X, nxt.row0, nxt.ntok);
       if (i + DEPTH < NS) {
         fetch(cur, i + DEPTH, ring[b]);
       } else {
-        // the next item's tokens go out ahead of its first weight step: loads complete in
-        // order, so the token store at the boundary waits for them alone.  After the block's
-        // last item nxt is the first item again (loads no one uses): branch-free, so the
-        // load counter stays exact
-        if (i + DEPTH == NS) tt.load(X, nxt.row0, nxt.ntok);
         fetch(nxt, i + DEPTH - NS, ring[b]);
       }
       __builtin_amdgcn_sched_barrier(0);
+      if (i == NS / 2 - (NS == 2 ? 0 : 1)) {
+        lds_wait_ge(&n_done, (uint32_t)(PF_GWPB * k));
+        tt.store(xs + ((k + 1) & 1) * BUF, F::paired);
+        lds_count(&n_stored);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if ((i + 1) % SPT != 0) continue;
       // end of tile t: per-row scale, then down stores y; gate_up up waves leave u in LDS,
       // gate waves keep g until the boundary
@@ -531,26 +557,27 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
           reinterpret_cast<float*>(out)[(cur.row0 + tok) * (size_t)N + n] = tA[r];
         }
       } else if (up) {
+        // ups[k & 1] held item k - 2, which every gate wave has read
+        lds_wait_ge(&n_gate, (uint32_t)(WR * (k > 0 ? k - 1 : 0)));
         ups[(((k & 1) * PF_GRPW + t) * WR + wt) * 64 + lane] = tA;
+        lds_count(&n_up);
       } else {
         pend.t[t] = tA, pend.col[t] = (int)n;
         pend.row0 = cur.row0, pend.ntok = cur.ntok, pend.valid = true;
       }
       tA = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    lds_count(&n_done);  // this wave is done with tile k (its LDS reads have returned)
     if (!nxt.valid) break;
-    // stage the next item's tokens into the other buffer (last read in item k - 1, which every
-    // wave finished before the previous boundary's barrier)
-    tt.store(xs + ((k + 1) & 1) * BUF, F::paired);
     cur = nxt;
     nxt = item_at(blockIdx.x + (k + 2) * gridDim.x);
-    lds_barrier();
+    // the next tile is complete once every wave stored its part
+    lds_wait_ge(&n_stored, (uint32_t)(PF_GWPB * (k + 1)));
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (MODE == 0) {
-    lds_barrier();
-    if (!up && pend.valid) finish_gate(pend, k);  // the last item
-  }
+  if (MODE == 0 && !up && pend.valid) finish_gate(pend, k);  // the last item
+  // no wave may leave while others still count on its LDS (the counters live in it)
+  lds_barrier();
 }
 
 

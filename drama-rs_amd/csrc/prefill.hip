@@ -4,25 +4,23 @@
 // Rows of xp are sorted by expert; expert e owns rows [offsets[e], offsets[e] + counts[e]).
 // gate_up: act[t] = bf16(silu(G_e . x_t) * (U_e . x_t)); down: y[t] = D_e . act_t (fp32).
 //
-// One wave owns a 16-row tile of weight rows (for gate_up: 16 gate rows and the 16 matching
-// up rows) and computes it against one 16-token pass of its expert with
-// v_mfma_f32_16x16x32_bf16: A = tokens (16 x 32), B = weights (32 x 16), D = 16 x 16 fp32, so
-// the four D values of a lane share one weight row and the per-row scale stays in a register.
-// Passes of one expert are spread over grid z; the 16 tokens of a pass sit in LDS (K x 16 bf16).
+// k_grouped (the routed experts): a wave owns a 16-row tile of weight rows and computes it
+// against a 16-token pass of its expert with v_mfma_f32_16x16x32_bf16: A = tokens (16 x 32),
+// B = weights (32 x 16), D = 16 x 16 fp32, so the four D values of a lane share one weight row.
 // Weights are dequantised exactly in registers: an int4 nibble q becomes the bf16 value
 // 128 + q (bit pattern 0x4300 | q), an int8 or fp8 value converts to bf16 exactly.  Each MFMA
 // stays inside one scale group, so per group g the fp32 product sum acc_g is rescaled:
 //   int4:  out += s_g acc_g + (m_g - 128 s_g) X_g,  X_g = sum of the group's inputs
 //   int8 / fp8:  out += s_g acc_g  (one scale per 128 inputs, or one per row at the end)
 // which is w = q s + m applied after exact integer x bf16 products: the same values as
-// dequantise-then-fp32, accumulated in fp32.  X_g comes from one more MFMA with bf16 ones.
+// dequantise-then-fp32, accumulated in fp32.
 //
-// Lane l of a wave holds, for MFMA step s (two per 64-wide group G), weight row (l % 16) and
-// the 8 inputs k = 64 G + 16 (l / 16) + 8 s + perm(t), t = 0..7, where perm = 0 4 1 5 2 6 3 7
-// is the order in which the nibble masking (w >> 4 j) & 0x000f000f produces bf16 pairs.  The
-// token tile in LDS is stored in the same permuted order, 16-byte chunk b of token t at
-// b ^ (t % 16) so the 16 token rows of one read spread over all banks; each A fragment is one
-// 16-byte LDS read.  Weight loads run two steps ahead of the MFMAs.
+// Fragment order: an MFMA lane holds 8 inputs in the order 0 4 1 5 2 6 3 7 of an 8-input
+// chunk, the order in which the nibble masking (w >> 4 j) & 0x000f000f (and the int8 / fp8
+// byte pairing) produces bf16 pairs; token tiles in LDS are stored in the same permuted
+// order, 16-byte chunk b of token t at b ^ (t % 16), so the 16 token rows of one read spread
+// over all banks and each A fragment is one 16-byte LDS read.  The per-kernel comments give
+// the lane -> input mapping of each weight format.
 #include <mutex>
 
 #include "common.hpp"
@@ -440,7 +438,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   };
   int k = 0;
   for (;; ++k) {
-    if (MODE == 0 && !up && pend.valid) finish_gate(pend, k - 1);
+    if (MODE == 0 && !up && pend.valid) finish_gate(pend, k - 1);  // (at mid-item: measured slower)
     const uint4* xb = xs + (k & 1) * BUF;
     const uint4* xrow = xb + (size_t)c16 * (K / 8);
     // int4 pairs: lanes g = 0, 1 carry the first group of a pair, g = 2, 3 the second; for the
@@ -535,7 +533,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
         fetch(nxt, i + DEPTH - NS, ring[b]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (i == NS / 2 - (NS == 2 ? 0 : 1)) {
+      if (i == (NS == 2 ? 1 : NS / 2 - 1)) {  // measured: step 3 of 8 (1, 2 and 5 slower)
         lds_wait_ge(&n_done, (uint32_t)(PF_GWPB * k));
         tt.store(xs + ((k + 1) & 1) * BUF, F::paired);
         lds_count(&n_stored);

@@ -197,6 +197,32 @@ DEV int canon_merge_topk32(int key, int e, int topk) {
   return id;
 }
 
+// Candidate (key, expert) as one integer ordered like the selection: larger key first, lower
+// expert first among equal keys.
+DEV uint64_t canon_cand64(int key, int e) {
+  return ((uint64_t)((uint32_t)key ^ 0x80000000u) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+DEV int canon_cand64_expert(uint64_t c) { return (int)(0xffffffffu - (uint32_t)c); }
+
+// The merge of canon_merge_topk32 computed as ranks, without rounds: candidate c (held by
+// lanes c and c + 32, c < 32) comes at pick position #{d : cand[d] > cand[c]} in the
+// canon_cand64 order, which is canon_merge_topk32's pick order (its ties go to the lowest
+// slot, which holds the lowest expert).  Valid candidates are distinct experts, so their
+// positions are distinct; padding candidates may repeat an expert but rank behind at least
+// topk valid ones whenever E >= topk.  Lanes c and c + 32 count 16 candidates each; every
+// lane returns the full rank of candidate lane % 32.  All 64 lanes must be active.
+DEV int canon_merge_rank32(const uint64_t* __restrict__ cand) {
+  const int lane = lane_id();
+  const uint64_t me = cand[lane & 31];
+  const uint64_t* h = cand + 16 * (lane >> 5);
+  int c[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) c[j & 3] += h[j] > me;
+  float a, b;
+  xchg<32>(__int_as_float((c[0] + c[1]) + (c[2] + c[3])), a, b);
+  return __float_as_int(a) + __float_as_int(b);
+}
+
 // Softmax denominator: m = max of the non-NaN logits, z = sum of canon_exp(l - m) with lane
 // l summing experts l + 64 j in order, then the xor butterfly.  Same bits on every lane.
 DEV float canon_softmax_z(const float* __restrict__ l, int E, float* m_out) {

@@ -104,6 +104,13 @@ DEV void wave_argmax(float& v, int& i) {
   xarg_step<32>(v, i);
 }
 
+// Workgroup barrier that orders LDS only: global loads in flight stay in flight across it.
+DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 DEV int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
 DEV int wave_id() { return (int)(threadIdx.x >> 6); }
 

@@ -147,18 +147,6 @@ struct Raw<FmtFP8<SF>> {
   using T = uint4;
 };
 
-// Token tile of tokens [row0, row0 + ntok) x all K inputs of a bf16 row matrix, staged into LDS
-// in the permuted fragment order: 16-byte block r of token t at t * K / 8 + (r ^ t), the xor
-// spreading the 16 tokens of one read over distinct LDS banks; rows beyond ntok are zero.
-// Split in two so the caller can issue its first weight loads between the token loads and
-// the LDS stores: the stores wait only for the token loads issued before those weight loads.
-// Workgroup barrier that orders LDS only: global loads in flight stay in flight across it.
-DEV void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Spin until an LDS counter reaches target (acquire); bounded, so a broken protocol ends the
 // wait instead of hanging the GPU (the results are then wrong, which the tests catch).
 DEV void lds_wait_ge(const uint32_t* c, uint32_t target) {
@@ -171,6 +159,11 @@ DEV void lds_count(uint32_t* c) {
   if (lane_id() == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Token tile of tokens [row0, row0 + ntok) x all K inputs of a bf16 row matrix, staged into LDS
+// in the permuted fragment order: 16-byte block r of token t at t * K / 8 + (r ^ t), the xor
+// spreading the 16 tokens of one read over distinct LDS banks; rows beyond ntok are zero.
+// Split in two so the caller can issue its first weight loads between the token loads and
+// the LDS stores: the stores wait only for the token loads issued before those weight loads.
 template <int K, int NT>
 struct TokTile {
   static constexpr int NB = PF_TOK * K / 8 / NT;  // 16-byte blocks per thread (NT threads)

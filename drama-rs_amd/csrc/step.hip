@@ -218,10 +218,10 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float4 xq4[H / 4];                        // normalised x in the int4 lane slots
   __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
   __shared__ float lg[ST_MAXE + 1];
-  __shared__ int s_sel[ST_TOPK];
+  __shared__ int s_sel[ST_WPB][ST_TOPK];  // every wave's copy of the picks
   __shared__ float s_asum[192];  // activation chunk sums (see SpecAct::post)
   __shared__ float s_xsum[64];   // sums of the 32-input chunks of xn (lane l's chunk)
-  __shared__ int2 s_cand[32];
+  __shared__ uint64_t s_cand[32];  // per-group top 8 (canon_cand64)
   __shared__ float s_mz[2];
   __shared__ int s_abort;
   __shared__ dr_decode_layer s_tab[ST_TABL];  // the first ST_TABL layer records
@@ -331,39 +331,27 @@ __global__ void __launch_bounds__(ST_NT, 1)
       if (!r && lane == 0) s_abort = 1;
       ST_PUT(8, r);
     }
+    // ---- top-k, first half: wave w < 4 has just polled (and stored) the logits of experts
+    // [64 w, 64 w + 64), so it selects their top 8 before the barrier
+    if (wave < 4) {
+      int ck, ce;
+      canon_select_group8(lg, E, wave, &ck, &ce);
+      if (lane < 8) s_cand[wave * 8 + lane] = canon_cand64(ck, ce);
+    }
     __syncthreads();
     ST_MARK(2);
     if (s_abort) return;
 
-    // ---- top-k: per-group top-8 on waves 0..3 and the softmax denominator on wave 4 side
-    // by side, then the merge of the 32 candidates on wave 0
-    if (wave < 4) {
-      int ck, ce;
-      canon_select_group8(lg, E, wave, &ck, &ce);
-      if (lane < 8) s_cand[wave * 8 + lane] = make_int2(ck, ce);
-    } else if (wave == 4) {
-      float m;
-      const float z = canon_softmax_z(lg, E, &m);
-      if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+    // ---- top-k, second half: the 32 candidates ranked by every wave (no second barrier);
+    // lane k < 8 of each wave's s_sel row receives pick k
+    {
+      const int rk8 = canon_merge_rank32(s_cand);
+      if (lane < 32 && rk8 < ST_TOPK) s_sel[wave][rk8] = canon_cand64_expert(s_cand[lane]);
     }
-    __syncthreads();
-    if (wave == 0) {
-      const int2 c = s_cand[lane & 31];
-      const int id = canon_merge_topk32(c.x, c.y, ST_TOPK);
-      if (lane < ST_TOPK) s_sel[lane] = id;
-    }
-    __syncthreads();
 
     {
-      const int my_idx = s_sel[lane & (ST_TOPK - 1)];
-      const float my_w = canon_topk_weight(lg[my_idx], s_mz[0], s_mz[1], ST_TOPK);
-      const float sgv = sigmoid(lg[E]);
+      const int my_idx = s_sel[wave][lane & (ST_TOPK - 1)];
       ST_MARK(3);
-      if (blockIdx.x == 0 && wave == 0) {
-        if (idx_out && lane < ST_TOPK) idx_out[l * ST_TOPK + lane] = my_idx;
-        if (wts_out && lane < ST_TOPK) wts_out[l * ST_TOPK + lane] = my_w;
-        if (sgate_out && lane == 0) sgate_out[l] = lg[E];
-      }
 
       // ---- routed weight loads: gate_up pairs, then the down row (8 experts + shared)
       const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
@@ -380,7 +368,14 @@ __global__ void __launch_bounds__(ST_NT, 1)
         su[p] = sm[(size_t)(I + j) * (H / 64)];
       }
       const size_t ea = (size_t)__shfl(my_idx, ka), eb = (size_t)__shfl(my_idx, 4 + ka);
-      const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
+      // the softmax denominator is needed only by the down phase: wave 4 computes it while
+      // its gate_up loads are in flight
+      __builtin_amdgcn_sched_barrier(0);
+      if (wave == 4) {
+        float m;
+        const float z = canon_softmax_z(lg, E, &m);
+        if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+      }
 
       // ---- gate_up: two routed pairs per wave
       {
@@ -442,7 +437,17 @@ __global__ void __launch_bounds__(ST_NT, 1)
           for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
         }
         if (is_shared) load_shared_pair<SH>(Ln, sj, lane, sp);
-        if (Ln.nw) nwv = reinterpret_cast<const float4*>(Ln.nw)[tid];
+        nwv = Ln.nw ? reinterpret_cast<const float4*>(Ln.nw)[tid] : make_float4(1.f, 1.f, 1.f, 1.f);
+      }
+
+      // ---- routing weights (s_mz is complete since the activation barrier)
+      const float my_w = canon_topk_weight(lg[my_idx], s_mz[0], s_mz[1], ST_TOPK);
+      const float sgv = sigmoid(lg[E]);
+      const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
+      if (blockIdx.x == 0 && wave == 0) {
+        if (idx_out && lane < ST_TOPK) idx_out[l * ST_TOPK + lane] = my_idx;
+        if (wts_out && lane < ST_TOPK) wts_out[l * ST_TOPK + lane] = my_w;
+        if (sgate_out && lane == 0) sgate_out[l] = lg[E];
       }
 
       // ---- down row n: 8 experts + shared, weighted, plus the residual

@@ -63,7 +63,7 @@ def check_stack(st, x0, idx, wts, sg, xs, x_final):
     np.testing.assert_array_equal(bits(x_final), bits(xs[-1]))
 
 
-@pytest.mark.parametrize("fmt,E,n", [("cfg", 256, 3), ("ref", 256, 2), ("cfg", 64, 4)])
+@pytest.mark.parametrize("fmt,E,n", [("cfg", 256, 3), ("ref", 256, 2), ("cfg", 64, 4), ("cfg", 8, 2)])
 def test_step_matches_oracle_layer_by_layer(fmt, E, n):
     print(f"step parity fmt={fmt} E={E} layers={n}", flush=True)
     st = Stack([300 + 7 * i for i in range(n)], E, fmt)
@@ -72,6 +72,25 @@ def test_step_matches_oracle_layer_by_layer(fmt, E, n):
     idx, wts, sg, xs = st.run(xd)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"
     check_stack(st, x0, idx, wts, sg, xs, host(xd))
+
+
+def test_step_tied_logits_pick_lowest_experts_first():
+    """Copies of the top expert's router row in other 64-expert groups and next to it give
+    exactly equal logits: the picks must come in (logit desc, expert asc) order, as the oracle's."""
+    st = Stack([91, 92], 256, "cfg")
+    x0 = np.random.default_rng(9).normal(0, 1, H).astype(np.float32)
+    L0 = st.h[0]
+    lg, ri, _, _ = O.router_topk(L0["router"], x0, L0["nw"], 1e-6, 256, TOPK)
+    top, second = int(ri[0]), int(ri[1])
+    for L, d in zip(st.h, st.d):
+        for dst in {(top + 1) % 256, (top + 64) % 256, (top + 130) % 256, (second + 200) % 256} - {top, second}:
+            L["router"][dst] = L["router"][top]
+        d["router"].copy_(dev(L["router"]))
+    _, ri2, _, _ = O.router_topk(L0["router"], x0, L0["nw"], 1e-6, 256, TOPK)
+    assert len(set(ri2[:4].tolist())) == 4 and top in ri2[:4].tolist()
+    xd = dev(x0)
+    r = st.run(xd)
+    check_stack(st, x0, *r, host(xd))
 
 
 def test_step_repeats_and_matches_first_call_bits():

@@ -41,12 +41,15 @@ constexpr int ST_NB = 256, ST_WPB = 8, ST_NT = ST_WPB * 64, ST_NP = 8;  // every
 constexpr uint32_t ST_TAG_STRIDE = 4096;
 constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
 constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the critical path cost ~1 us)
-// Polling too early slows an exchange down: polls of 2048 waves that reach the memory side
-// before the producers' stores contend with them (measured on MI355X, configuration 3: the
-// layer went from 20.3 to 15.8 us with these delays).  So each wave issues its first poll of
-// an exchange this many 10 ns ticks after it reaches the exchange, and waits a little
-// between rounds.
-constexpr uint32_t ST_DLY_LOGITS = 120, ST_DLY_ACT = 160, ST_DLY_X = 120, ST_DLY_ROUND = 20;
+// When each wave polls an exchange for the first time, in 10 ns ticks of s_memrealtime after
+// a point every wave of the block passes together (so the waves that reach an exchange early,
+// like the non-router waves at the logits, do not poll before the data can be there): the
+// logits after the layer start, the activations after top-k, the residual after the
+// activation barrier.  A poll that comes too early costs a whole extra round trip, and early
+// polls slow the exchange for everybody; these offsets were measured on MI355X
+// (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
+// 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
+constexpr uint32_t ST_OFF_LOGITS = 185, ST_OFF_ACT = 370, ST_OFF_X = 285, ST_DLY_ROUND = 20;
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
@@ -91,22 +94,22 @@ DEV float2 ll_val2(uint64_t w) {
   return make_float2(__uint_as_float((uint32_t)(w >> 16) & 0xffffff00u), __uint_as_float((uint32_t)(w << 8)));
 }
 
-DEV void wait_ticks(uint32_t n) {
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  while (__builtin_amdgcn_s_memrealtime() - t0 < n) __builtin_amdgcn_s_sleep(1);
+DEV void wait_until(uint64_t t) {
+  while (__builtin_amdgcn_s_memrealtime() < t) __builtin_amdgcn_s_sleep(1);
 }
+DEV void wait_ticks(uint32_t n) { wait_until(__builtin_amdgcn_s_memrealtime() + n); }
 
 // LDS float4 slots: int4 rows give lane l the 32 inputs [32 l, 32 l + 32) -> slot i * 64 + l
 DEV int slot_q4(int f) { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
 
 // Wave share of an exchange: wave p of NP owns, in lane l, the words base[l + 64 r] of rows
-// r = p + NP i, i < N.  It reloads the words whose tag is not yet the phase's until all are
-// current, then hands each to spec.store.  Returns the rounds taken, 0 after ~0.2 s (the
+// r = p + NP i, i < N.  It reads them first at s_memrealtime first_poll, reloads the words
+// whose tag is not yet the phase's until all are current, then hands each to spec.store.  Returns the rounds taken, 0 after ~0.2 s (the
 // caller aborts).
 template <int N, int NP, class Spec>
-DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync, uint32_t first_delay) {
+DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync, uint64_t first_poll) {
   const int lane = lane_id();
-  wait_ticks(first_delay);
+  wait_until(first_poll);
   const uint64_t* b = base + lane + 64 * p;
   uint64_t v[N];
 #pragma unroll
@@ -272,6 +275,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
     const dr_decode_layer Ly = layer(l);
     const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2;
     ST_MARK(0);
+    const uint64_t t_layer = __builtin_amdgcn_s_memrealtime();
     float res;  // x[n], read now: the poller overwrites xr4 during the down phase
 
     // ---- RMSNorm (canonical, every wave) and the router row; the poller collects logits
@@ -327,7 +331,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(1);
     }
     if (poller) {
-      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, ST_DLY_LOGITS);
+      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, t_layer + ST_OFF_LOGITS);
       if (!r && lane == 0) s_abort = 1;
       ST_PUT(8, r);
     }
@@ -352,6 +356,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
     {
       const int my_idx = s_sel[wave][lane & (ST_TOPK - 1)];
       ST_MARK(3);
+      const uint64_t t_topk = __builtin_amdgcn_s_memrealtime();
 
       // ---- routed weight loads: gate_up pairs, then the down row (8 experts + shared)
       const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
@@ -416,7 +421,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4), s_asum}, sync, ST_DLY_ACT);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + ST_OFF_ACT);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -425,6 +430,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
       __syncthreads();
       ST_MARK(5);
+      const uint64_t t_act = __builtin_amdgcn_s_memrealtime();
       if (s_abort) return;
 
       // ---- next layer's known weights: issued after the activation poll (a wave's loads
@@ -484,7 +490,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
-        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, ST_DLY_X);
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + ST_OFF_X);
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }

@@ -161,12 +161,9 @@ DEV int canon_select_topk(const float* __restrict__ l, int E, int topk) {
 
 // The same selection in two phases for topk <= 8 and E <= 256, spread over four waves.
 // Phase 1, wave w (w < 4): the top-8 of experts [64 w, 64 w + 64) (one per lane), in pick
-// order; lane r < 8 returns pick r as (key, expert).  Phase 2, one wave: lane c < 32 holds
-// candidate c = 8 w + r; the top-k of the 32 candidates is the top-k of all E experts (each
-// group contributes at most 8), and among equal keys a lower candidate slot always holds the
-// lower expert (within a group equal keys are picked in index order, groups are in index
-// order), so lowest slot first reproduces (key desc, index asc).  Lane k < topk returns the
-// expert of pick k.
+// order; lane r < 8 returns pick r as (key, expert), candidate c = 8 w + r.  The top-k of the
+// 32 candidates is the top-k of all E experts (each group contributes at most 8); phase 2,
+// canon_merge_rank32, orders them.
 DEV void canon_select_group8(const float* __restrict__ l, int E, int w, int* cand_key, int* cand_e) {
   const int lane = lane_id();
   const int e = 64 * w + lane;
@@ -183,20 +180,6 @@ DEV void canon_select_group8(const float* __restrict__ l, int E, int w, int* can
   *cand_e = ce;
 }
 
-DEV int canon_merge_topk32(int key, int e, int topk) {
-  const int lane = lane_id();
-  if (lane >= 32) key = KEY_PAD;
-  int id = 0;
-  for (int k = 0; k < topk; ++k) {
-    const int kb = wave_max_i(key);
-    const int ls = (int)__builtin_ctzll(__ballot(key == kb));
-    const int eb = __builtin_amdgcn_readlane(e, ls);
-    if (lane == ls) key = KEY_PICKED;
-    if (lane == k) id = eb;
-  }
-  return id;
-}
-
 // Candidate (key, expert) as one integer ordered like the selection: larger key first, lower
 // expert first among equal keys.
 DEV uint64_t canon_cand64(int key, int e) {
@@ -204,13 +187,15 @@ DEV uint64_t canon_cand64(int key, int e) {
 }
 DEV int canon_cand64_expert(uint64_t c) { return (int)(0xffffffffu - (uint32_t)c); }
 
-// The merge of canon_merge_topk32 computed as ranks, without rounds: candidate c (held by
-// lanes c and c + 32, c < 32) comes at pick position #{d : cand[d] > cand[c]} in the
-// canon_cand64 order, which is canon_merge_topk32's pick order (its ties go to the lowest
-// slot, which holds the lowest expert).  Valid candidates are distinct experts, so their
-// positions are distinct; padding candidates may repeat an expert but rank behind at least
-// topk valid ones whenever E >= topk.  Lanes c and c + 32 count 16 candidates each; every
-// lane returns the full rank of candidate lane % 32.  All 64 lanes must be active.
+// Phase 2, the merge of the 32 candidates, computed as ranks without rounds: candidate c
+// (held by lanes c and c + 32, c < 32) is pick #{d : cand[d] > cand[c]} in the canon_cand64
+// order (key desc, expert asc), the order in which k rounds of "largest key, lowest slot
+// among equals" would pick them: within a group equal keys are picked in index order and the
+// groups are in index order, so a lower slot holds the lower expert.  Valid candidates are
+// distinct experts, so their ranks are distinct; padding candidates may repeat an expert but
+// rank behind at least topk valid ones whenever E >= topk.  Lanes c and c + 32 count 16
+// candidates each; every lane returns the full rank of candidate lane % 32.  All 64 lanes
+// must be active.
 DEV int canon_merge_rank32(const uint64_t* __restrict__ cand) {
   const int lane = lane_id();
   const uint64_t me = cand[lane & 31];

@@ -14,13 +14,23 @@ namespace {
 
 constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
 
+// Pick k < topk <= 8 of the 32 group candidates, by rank (canon_merge_rank32): the candidate
+// of rank k is written to sel[k] and read back by lane k.  One wave, all lanes active.
+DEV int merge_picks(const uint64_t* cand, int* sel, int topk) {
+  const int lane = lane_id();
+  const int rk = canon_merge_rank32(cand);
+  if (lane < 32 && rk < topk) sel[rk] = canon_cand64_expert(cand[lane]);
+  return lane < topk ? sel[lane] : 0;
+}
+
 // Decode router: wave w of block b computes logit row RT_WPB b + w of the E + 1 rows.  All
 // loads of a wave (its weight row, x for the norm, x and nw for its dot lanes) are issued
 // before any arithmetic.  Logits are published with cache-bypassing (sc1) stores; after its
 // stores have completed (s_waitcnt) each block counts itself in with one relaxed atomic, and
-// the last block reads the logits back with sc1 loads and runs softmax/top-k (two-phase
-// selection on four waves for topk <= 8).  No cache-maintenance fence is needed: every cross-block value bypasses the
+// the last block reads the logits back with sc1 loads and runs softmax/top-k (group
+// selections on four waves and a rank merge for topk <= 8).  No cache-maintenance fence is needed: every cross-block value bypasses the
 // non-coherent caches.  The last block resets the counter for the next call.
+
 template <int K>
 __global__ void __launch_bounds__(RT_WPB * 64)
     k_router_topk(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ nw,
@@ -68,7 +78,8 @@ __global__ void __launch_bounds__(RT_WPB * 64)
   // stage the logits (sc1 loads) in LDS, then the canonical softmax/top-k: for topk <= 8 the
   // group selections on waves 0..3 and the denominator on wave 4 run side by side
   __shared__ float lg[257];
-  __shared__ int2 s_cand[32];
+  __shared__ uint64_t s_cand[32];
+  __shared__ int s_sel[8];
   __shared__ float s_mz[2];
   if ((int)threadIdx.x <= E) lg[threadIdx.x] = __hip_atomic_load(logits + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
@@ -76,7 +87,7 @@ __global__ void __launch_bounds__(RT_WPB * 64)
     if (wave < 4) {
       int ck, ce;
       canon_select_group8(lg, E, wave, &ck, &ce);
-      if (lane < 8) s_cand[wave * 8 + lane] = make_int2(ck, ce);
+      if (lane < 8) s_cand[wave * 8 + lane] = canon_cand64(ck, ce);
     } else if (wave == 4) {
       float m;
       const float z = canon_softmax_z(lg, E, &m);
@@ -84,8 +95,7 @@ __global__ void __launch_bounds__(RT_WPB * 64)
     }
     __syncthreads();
     if (wave != 0) return;
-    const int2 c = s_cand[lane & 31];
-    const int id = canon_merge_topk32(c.x, c.y, topk);
+    const int id = merge_picks(s_cand, s_sel, topk);
     const float w = canon_topk_weight(lg[lane < topk ? id : 0], s_mz[0], s_mz[1], topk);
     if (lane < topk) idx[lane] = id, wts[lane] = w;
   } else {
@@ -110,7 +120,8 @@ __global__ void __launch_bounds__(320)
   const int r = blockIdx.x, lane = lane_id(), wave = wave_id();
   const float* l = logits + (size_t)r * stride;
   __shared__ float lg[257];
-  __shared__ int2 s_cand[32];
+  __shared__ uint64_t s_cand[32];
+  __shared__ int s_sel[8];
   __shared__ float s_mz[2];
   if ((int)threadIdx.x <= E) lg[threadIdx.x] = l[threadIdx.x];
   __syncthreads();
@@ -119,7 +130,7 @@ __global__ void __launch_bounds__(320)
     if (wave < 4) {
       int ck, ce;
       canon_select_group8(lg, E, wave, &ck, &ce);
-      if (lane < 8) s_cand[wave * 8 + lane] = make_int2(ck, ce);
+      if (lane < 8) s_cand[wave * 8 + lane] = canon_cand64(ck, ce);
     } else {
       float m;
       const float z = canon_softmax_z(lg, E, &m);
@@ -127,8 +138,7 @@ __global__ void __launch_bounds__(320)
     }
     __syncthreads();
     if (wave != 0) return;
-    const int2 c = s_cand[lane & 31];
-    const int id = canon_merge_topk32(c.x, c.y, topk);
+    const int id = merge_picks(s_cand, s_sel, topk);
     const float w = canon_topk_weight(lg[lane < topk ? id : 0], s_mz[0], s_mz[1], topk);
     if (lane < topk) idx[(size_t)r * topk + lane] = id, wts[(size_t)r * topk + lane] = w;
   } else {

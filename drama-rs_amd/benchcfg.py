@@ -238,6 +238,27 @@ def config5_fp8(lib, st, iters=100, copies=4):
     out["decode_batch1"] = rec(ms * 1000, b1, us_graph=round(msg * 1000, 2),
                                note="router + fp8 gate_up + down + int8 shared; x evolves per call; 4 layer copies "
                                     "rotated; us_graph: the same calls replayed from a HIP graph")
+    # the fused persistent step over 40 layers: layer l has its own router (so the routing
+    # differs from layer to layer) and the experts of copy l % copies (a layer's 8 experts are
+    # one of 4 x 256 3-MiB blocks, so few are still in the MALL from an earlier layer)
+    keys = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")
+    nl = 40
+    gr = torch.Generator(device="cuda").manual_seed(43)
+    routers = [bf16_bits(torch.randn(E + 1, H, generator=gr, device="cuda") * 0.02) for _ in range(nl)]
+    table = torch.tensor([[(routers[l] if k == "router" else Ls[l % copies][k]).data_ptr() for k in keys]
+                          for l in range(nl)], dtype=torch.int64, device="cuda")
+    ll, sync = z(6920, torch.int64), z(4, torch.int32)
+
+    def fused(i):
+        lib.dr_moe_decode_step_fp8_bf16s(P(table), nl, P(x), E, H, I, TOPK, 1e-6, P(ll), P(sync), None, None, None,
+                                         None, sp)
+
+    msf = timed(fused, max(1, iters // 10), st)
+    if int(sync[1].item()) != 0:
+        raise RuntimeError("dr_moe_decode_step_fp8_bf16s timed out")
+    out["decode_batch1_fused"] = rec(msf * 1000 / nl, b1,
+                                     note=f"{nl} layers (own router each, experts of copy l % {copies}) in one "
+                                          "dr_moe_decode_step_fp8_bf16s launch; us per layer")
     # batch 4 through the grouped (prefill) path: union of up to 32 experts
     pf = Prefill(4, st)
 
@@ -250,7 +271,7 @@ def config5_fp8(lib, st, iters=100, copies=4):
     nb4, hit = pf.layer_bytes(L)
     out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, us_graph=round(ms4g * 1000, 2),
                                note="4 rows via the grouped MFMA path (bf16 act); us_graph: replayed from a HIP graph")
-    del L, Ls
+    del L, Ls, routers
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections
     g = torch.Generator(device="cuda").manual_seed(51)

@@ -111,6 +111,28 @@ DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Block-FP8 helpers: one scale per 128 x 128 block, f32 (SF = 0, the reference's scale_inv)
+// or bf16 (SF = 1); e4m3 bytes convert to f32 exactly with v_cvt_pk_f32_fp8.
+template <int SF>
+DEV float blk_scale(const void* S, size_t i) {
+  return SF ? bf16f(reinterpret_cast<const uint16_t*>(S)[i]) : reinterpret_cast<const float*>(S)[i];
+}
+
+// sum_{i<16} e4m3(w bytes) * x[i]
+DEV float dot16_fp8(const uint4& w, const float* x, float acc) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], true);
+    acc = __builtin_fmaf(lo[0], x[4 * d + 0], acc);
+    acc = __builtin_fmaf(lo[1], x[4 * d + 1], acc);
+    acc = __builtin_fmaf(hi[0], x[4 * d + 2], acc);
+    acc = __builtin_fmaf(hi[1], x[4 * d + 3], acc);
+  }
+  return acc;
+}
+
 DEV int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
 DEV int wave_id() { return (int)(threadIdx.x >> 6); }
 

@@ -20,26 +20,6 @@ constexpr int G8_NB_ROUTED = TOPK8 * I8 / (G8_WPB * G8_PPW);
 constexpr int G8_NB_SHARED = I8 / G8_WPB;
 constexpr int D8_WPB = 4, D8_RPW = 2;
 
-template <int SF>
-DEV float blk_scale(const void* S, size_t i) {
-  return SF ? bf16f(reinterpret_cast<const uint16_t*>(S)[i]) : reinterpret_cast<const float*>(S)[i];
-}
-
-// sum_{i<16} e4m3(w bytes) * x[i]
-DEV float dot16_fp8(const uint4& w, const float* x, float acc) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], false);
-    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(ww[d], true);
-    acc = __builtin_fmaf(lo[0], x[4 * d + 0], acc);
-    acc = __builtin_fmaf(lo[1], x[4 * d + 1], acc);
-    acc = __builtin_fmaf(hi[0], x[4 * d + 2], acc);
-    acc = __builtin_fmaf(hi[1], x[4 * d + 3], acc);
-  }
-  return acc;
-}
-
 DEV float dot16_u8b(const uint4& w, const float* x, float acc) {
   acc = dot4_u8b(w.x, x, acc);
   acc = dot4_u8b(w.y, x + 4, acc);

@@ -1,8 +1,9 @@
-// Fused batch-1 decode step: router, top-k, int4 gate_up + SiLU*up, down + weighted combine
-// and the int8 shared expert of n_layers MoE layers in ONE persistent launch.  It computes
-// exactly what the engine's per-layer chain dr_router_topk -> dr_moe_decode computes
-// (reference: src/engine.rs:1001-1007 recording kernels/drama.cu:369-461,470-599 per layer),
-// with routing bit-exact to the canonical router order of canon.hpp.
+// Fused batch-1 decode step: router, top-k, gate_up + SiLU*up, down + weighted combine and
+// the int8 shared expert of n_layers MoE layers in ONE persistent launch, with int4 or
+// block-FP8 routed experts.  It computes exactly what the engine's per-layer chain
+// dr_router_topk -> dr_moe_decode (or dr_moe_decode_fp8) computes (reference:
+// src/engine.rs:1001-1007 recording kernels/drama.cu:369-461,470-742 per layer), with routing
+// bit-exact to the canonical router order of canon.hpp.
 //
 // Why one launch: a layer streams ~18 MB, 2.3 us at the HBM roofline, while each dependent
 // launch costs ~1.5 us on MI355X before its first load issues.  Here 256 workgroups (one per
@@ -49,7 +50,7 @@ constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the
 // polls slow the exchange for everybody; these offsets were measured on MI355X
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
-constexpr uint32_t ST_OFF_LOGITS = 185, ST_OFF_ACT = 370, ST_OFF_X = 285, ST_DLY_ROUND = 20;
+constexpr uint32_t ST_OFF_LOGITS = 185, ST_DLY_ROUND = 20;  // the other two offsets depend on the format
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
@@ -155,11 +156,13 @@ struct Spec32 {
 };
 
 // activations: words 0..2047 hold routed elements 2w, 2w + 1 (packed, i < 32), words
-// 2048..2559 shared element w - 2048 (one per word, i >= 32); stored into the down slots
+// 2048..2559 shared element w - 2048 (one per word, i >= 32); stored into the down slots of
+// the weight format F
+template <class F>
 struct SpecAct {
   uint32_t tag;
   float* dst;   // as4 as floats
-  float* sums;  // [0, 128): sums of the 32-element routed chunks, [128, 192): of the 8-element shared chunks
+  float* sums;  // [0, 128): sums of the 32-element routed chunks (int4), [128, 192): of the 8-element shared chunks
   DEV bool valid(int r, int) const { return r < 40; }
   DEV uint64_t ready(int i) const { return i < 32 ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32; }
   DEV bool ok(int i, uint64_t v) const {
@@ -168,27 +171,197 @@ struct SpecAct {
   DEV void store(int i, int w, uint64_t v) const {
     if (i < 32) {
       const float2 p = ll_val2(v);
-      float* d = dst + slot_q4(w >> 1) * 4 + (w & 1) * 2;
+      float* d = F::act_pair(dst, w);
       d[0] = p.x, d[1] = p.y;
     } else {
       const int e = w - 2048;
       dst[(1024 + ((e >> 2) & 1) * 64 + (e >> 3)) * 4 + (e & 3)] = __uint_as_float((uint32_t)v);
     }
   }
-  // chunk sums for the down dot's min term: a routed chunk is 16 consecutive words (lanes) of
-  // one row, a shared chunk 8 consecutive words
+  // chunk sums for the down dots' min terms: an int4 routed chunk is 16 consecutive words
+  // (lanes) of one row, a shared chunk 8 consecutive words
   DEV void post(int r, uint64_t v) const {
     const int lane = lane_id();
     if (r < 32) {
-      const float2 p = ll_val2(v);
-      float t = p.x + p.y;
-      t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t);
-      if ((lane & 15) == 0) sums[4 * r + (lane >> 4)] = t;
+      if constexpr (F::kMinTerm) {
+        const float2 p = ll_val2(v);
+        float t = p.x + p.y;
+        t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t);
+        if ((lane & 15) == 0) sums[4 * r + (lane >> 4)] = t;
+      }
     } else {
       float t = __uint_as_float((uint32_t)v);
       t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
       if ((lane & 7) == 0) sums[128 + 8 * (r - 32) + (lane >> 3)] = t;
     }
+  }
+};
+
+// Routed-expert weight formats of the step.  Each gives the lane slots of the normalised
+// input (xslot), the two (gate, up) pairs rj, rj + 1 of one expert per wave (load_gu, then
+// gate_up: the activations of both pairs), output row n of the 8 experts' down projections
+// (load_dn, then down: the weighted sum of the 8 dots, without the shared expert) and where
+// routed activation word w lands in the down slots (act_pair).
+//
+// int4 (scale, min) groups of 64: a 1024-byte gate_up row is one 16-byte load per lane,
+// lane l holding inputs [32 l, 32 l + 32); a 256-byte down row is 16 chunks, lane l holding
+// chunk l & 15 of experts l >> 4 and 4 + (l >> 4).
+template <class SC>
+struct StepQ4 {
+  static constexpr bool kMinTerm = true;
+  static constexpr uint32_t kOffAct = 370, kOffX = 285;  // first-poll offsets (measured)
+  DEV static int xslot(int f) { return slot_q4(f); }
+  struct GU {
+    uint4 wg[2], wu[2];
+    uint32_t sg[2], su[2];
+  };
+  DEV static void load_gu(const dr_decode_layer& Ly, size_t ek, int rj, int lane, GU& g) {
+    constexpr int H = ST_H, I = ST_I;
+    const uint8_t* q = Ly.gu_q + ek * (2 * I) * (H / 2) + lane * 16;
+    const uint32_t* sm = reinterpret_cast<const uint32_t*>(Ly.gu_s) + ek * (2 * I) * (H / 64) + (lane >> 1);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int j = rj + p;
+      g.wg[p] = ld16(q + (size_t)j * (H / 2));
+      g.wu[p] = ld16(q + (size_t)(I + j) * (H / 2));
+      g.sg[p] = sm[(size_t)j * (H / 64)];
+      g.su[p] = sm[(size_t)(I + j) * (H / 64)];
+    }
+  }
+  DEV static void gate_up(const GU& g, const float4* xq4, const float* s_xsum, int lane, float (&av)[2]) {
+    float xv[32];
+    const float xsum = s_xsum[lane];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = xq4[i * 64 + lane];
+      xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float qg = 0.f, qu = 0.f;
+      qg = dot8_q4(g.wg[p].x, xv + 0, qg), qu = dot8_q4(g.wu[p].x, xv + 0, qu);
+      qg = dot8_q4(g.wg[p].y, xv + 8, qg), qu = dot8_q4(g.wu[p].y, xv + 8, qu);
+      qg = dot8_q4(g.wg[p].z, xv + 16, qg), qu = dot8_q4(g.wu[p].z, xv + 16, qu);
+      qg = dot8_q4(g.wg[p].w, xv + 24, qg), qu = dot8_q4(g.wu[p].w, xv + 24, qu);
+      const float2 a = SC::pair(g.sg[p]), b = SC::pair(g.su[p]);
+      const float gv = wave_sum(a.x * qg + a.y * xsum);
+      const float uv = wave_sum(b.x * qu + b.y * xsum);
+      av[p] = silu(gv) * uv;
+    }
+  }
+  struct DN {
+    uint4 qa, qb;
+    uint32_t sa, sb;
+  };
+  DEV static void load_dn(const dr_decode_layer& Ly, int my_idx, int n, int lane, DN& d) {
+    constexpr int H = ST_H, I = ST_I;
+    const int ka = lane >> 4, cc = lane & 15;
+    const size_t ea = (size_t)__shfl(my_idx, ka), eb = (size_t)__shfl(my_idx, 4 + ka);
+    const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
+    d.qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
+    d.qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
+    d.sa = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
+    d.sb = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
+  }
+  DEV static float down(const DN& d, const float4* as4, const float* s_asum, float my_w, int lane) {
+    const int ka = lane >> 4;
+    const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
+    float xa[32], xb[32];
+    const float suma = s_asum[lane], sumb = s_asum[64 + lane];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = as4[i * 64 + lane], w = as4[512 + i * 64 + lane];
+      xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+      xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+    }
+    float da = 0.f, db = 0.f;
+    da = dot8_q4(d.qa.x, xa + 0, da), db = dot8_q4(d.qb.x, xb + 0, db);
+    da = dot8_q4(d.qa.y, xa + 8, da), db = dot8_q4(d.qb.y, xb + 8, db);
+    da = dot8_q4(d.qa.z, xa + 16, da), db = dot8_q4(d.qb.z, xb + 16, db);
+    da = dot8_q4(d.qa.w, xa + 24, da), db = dot8_q4(d.qb.w, xb + 24, db);
+    const float2 pa = SC::pair(d.sa), pb = SC::pair(d.sb);
+    return wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb);
+  }
+  DEV static float* act_pair(float* as4f, int w) { return as4f + slot_q4(w >> 1) * 4 + (w & 1) * 2; }
+};
+
+// Block-FP8 (e4m3, one scale per 128 x 128 block, f32 for SF = 0, bf16 for SF = 1): a
+// 2048-byte gate_up row is two 16-byte loads per lane (bytes [16 l, 16 l + 16) and
+// [1024 + 16 l, ...), the int8 shared layout); a 512-byte down row is 32 chunks, lane l
+// holding chunk l & 31 of experts 2 i + (l >> 5), i < 4.  Every 16-byte chunk lies in one
+// scale block.
+template <int SF>
+struct StepFP8 {
+  static constexpr bool kMinTerm = false;
+  static constexpr uint32_t kOffAct = 430, kOffX = 245;  // twice the gate_up bytes of int4 (measured)
+  DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
+  struct GU {
+    uint4 g[2][2], u[2][2];
+    float sg[2][2], su[2][2];
+  };
+  DEV static void load_gu(const dr_decode_layer& Ly, size_t ek, int rj, int lane, GU& g) {
+    constexpr int H = ST_H, I = ST_I;
+    const uint8_t* w = Ly.gu_q + ek * (2 * I) * H + lane * 16;
+    const size_t sb = ek * (size_t)(2 * I / 128) * (H / 128) + (lane >> 3);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int j = rj + p;
+      g.g[p][0] = ld16(w + (size_t)j * H), g.g[p][1] = ld16(w + (size_t)j * H + 1024);
+      g.u[p][0] = ld16(w + (size_t)(I + j) * H), g.u[p][1] = ld16(w + (size_t)(I + j) * H + 1024);
+      g.sg[p][0] = blk_scale<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128));
+      g.sg[p][1] = blk_scale<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128) + 8);
+      g.su[p][0] = blk_scale<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128));
+      g.su[p][1] = blk_scale<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128) + 8);
+    }
+  }
+  DEV static void gate_up(const GU& g, const float4* xq4, const float*, int lane, float (&av)[2]) {
+    float xa[16], xb[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = xq4[i * 64 + lane], w = xq4[256 + i * 64 + lane];
+      xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+      xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const float gv = wave_sum(g.sg[p][0] * dot16_fp8(g.g[p][0], xa, 0.f) + g.sg[p][1] * dot16_fp8(g.g[p][1], xb, 0.f));
+      const float uv = wave_sum(g.su[p][0] * dot16_fp8(g.u[p][0], xa, 0.f) + g.su[p][1] * dot16_fp8(g.u[p][1], xb, 0.f));
+      av[p] = silu(gv) * uv;
+    }
+  }
+  struct DN {
+    uint4 q[4];
+    float sc[4];
+  };
+  DEV static void load_dn(const dr_decode_layer& Ly, int my_idx, int n, int lane, DN& d) {
+    constexpr int H = ST_H, I = ST_I;
+    const int half = lane >> 5, cc = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const size_t e = (size_t)__shfl(my_idx, 2 * i + half);
+      d.q[i] = ld16(Ly.d_q + (e * H + n) * I + cc * 16);
+      d.sc[i] = blk_scale<SF>(Ly.d_s, (e * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
+    }
+  }
+  DEV static float down(const DN& d, const float4* as4, const float*, float my_w, int lane) {
+    const int half = lane >> 5;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float xa[16];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 v = as4[256 * i + t * 64 + lane];
+        xa[4 * t] = v.x, xa[4 * t + 1] = v.y, xa[4 * t + 2] = v.z, xa[4 * t + 3] = v.w;
+      }
+      acc += __shfl(my_w, 2 * i + half) * d.sc[i] * dot16_fp8(d.q[i], xa, 0.f);
+    }
+    return acc;
+  }
+  // routed element m (even) of expert slot k -> float 4 (256 (k >> 1) + 64 t + 32 (k & 1) + m / 16) + m % 4
+  DEV static float* act_pair(float* as4f, int w) {
+    const int k = w >> 8, m = 2 * (w & 255);
+    return as4f + (256 * (k >> 1) + ((m & 15) >> 2) * 64 + (k & 1) * 32 + (m >> 4)) * 4 + (m & 3);
   }
 };
 
@@ -210,7 +383,7 @@ DEV void load_shared_pair(const dr_decode_layer& Ly, int j, int lane, SharedPair
   s.su0 = SH::scale(Ly.sgu_s, I + j, lane * 16, H), s.su1 = SH::scale(Ly.sgu_s, I + j, 1024 + lane * 16, H);
 }
 
-template <class SC, class SH>
+template <class F, class SH>
 __global__ void __launch_bounds__(ST_NT, 1)
     k_decode_step(const dr_decode_layer* __restrict__ layers, int L, float* x, int E, float eps,
                   uint64_t* __restrict__ ll, uint32_t* __restrict__ sync, int* __restrict__ idx_out,
@@ -218,12 +391,12 @@ __global__ void __launch_bounds__(ST_NT, 1)
   constexpr int H = ST_H, I = ST_I;
   __shared__ float4 xr4[H / 4];                        // residual stream x (raw)
   __shared__ float4 nws[H / 4];                        // RMSNorm weight of the layer
-  __shared__ float4 xq4[H / 4];                        // normalised x in the int4 lane slots
+  __shared__ float4 xq4[H / 4];                        // normalised x in the F::xslot lane slots
   __shared__ float4 as4[(ST_TOPK + 1) * I / 4];        // activations in the down lane slots
   __shared__ float lg[ST_MAXE + 1];
   __shared__ int s_sel[ST_WPB][ST_TOPK];  // every wave's copy of the picks
   __shared__ float s_asum[192];  // activation chunk sums (see SpecAct::post)
-  __shared__ float s_xsum[64];   // sums of the 32-input chunks of xn (lane l's chunk)
+  __shared__ float s_xsum[64];   // int4: sums of the 32-input chunks of xn (lane l's chunk)
   __shared__ uint64_t s_cand[32];  // per-group top 8 (canon_cand64)
   __shared__ float s_mz[2];
   __shared__ int s_abort;
@@ -242,7 +415,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
   const int sj = g >> 2;               // shared gate_up pair
   const int rk = g >> 8;               // routed expert slot of the gate_up pairs
   const int rj = (2 * g) & (I - 1);    // first of the two gate_up pairs
-  const int ka = lane >> 4, cc = lane & 15;  // down: lane's expert slots ka, 4 + ka and chunk
   const int n = g;                     // down output row
 
   RouterRow rw;
@@ -287,10 +459,12 @@ __global__ void __launch_bounds__(ST_NT, 1)
       const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
       {
         const float4 xn = canon_norm4(xr4[tid], inv, nwv);
-        xq4[slot_q4(tid)] = xn;
-        float t = (xn.x + xn.y) + (xn.z + xn.w);  // threads 8c..8c+7 hold chunk c
-        t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
-        if ((lane & 7) == 0) s_xsum[tid >> 3] = t;
+        xq4[F::xslot(tid)] = xn;
+        if constexpr (F::kMinTerm) {
+          float t = (xn.x + xn.y) + (xn.z + xn.w);  // threads 8c..8c+7 hold chunk c
+          t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
+          if ((lane & 7) == 0) s_xsum[tid >> 3] = t;
+        }
       }
       if (is_router) {
         float4 a[4], b[4];
@@ -360,19 +534,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
       // ---- routed weight loads: gate_up pairs, then the down row (8 experts + shared)
       const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
-      const uint8_t* q = Ly.gu_q + ek * (2 * I) * (H / 2) + lane * 16;
-      const uint32_t* sm = reinterpret_cast<const uint32_t*>(Ly.gu_s) + ek * (2 * I) * (H / 64) + (lane >> 1);
-      uint4 wg[2], wu[2];
-      uint32_t sg[2], su[2];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const int j = rj + p;
-        wg[p] = ld16(q + (size_t)j * (H / 2));
-        wu[p] = ld16(q + (size_t)(I + j) * (H / 2));
-        sg[p] = sm[(size_t)j * (H / 64)];
-        su[p] = sm[(size_t)(I + j) * (H / 64)];
-      }
-      const size_t ea = (size_t)__shfl(my_idx, ka), eb = (size_t)__shfl(my_idx, 4 + ka);
+      typename F::GU gu;
+      F::load_gu(Ly, ek, rj, lane, gu);
       // the softmax denominator is needed only by the down phase: wave 4 computes it while
       // its gate_up loads are in flight
       __builtin_amdgcn_sched_barrier(0);
@@ -384,36 +547,15 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
       // ---- gate_up: two routed pairs per wave
       {
-        float xv[32];
-        const float xsum = s_xsum[lane];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float4 v = xq4[i * 64 + lane];
-          xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
-        }
         float av[2];
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          float qg = 0.f, qu = 0.f;
-          qg = dot8_q4(wg[p].x, xv + 0, qg), qu = dot8_q4(wu[p].x, xv + 0, qu);
-          qg = dot8_q4(wg[p].y, xv + 8, qg), qu = dot8_q4(wu[p].y, xv + 8, qu);
-          qg = dot8_q4(wg[p].z, xv + 16, qg), qu = dot8_q4(wu[p].z, xv + 16, qu);
-          qg = dot8_q4(wg[p].w, xv + 24, qg), qu = dot8_q4(wu[p].w, xv + 24, qu);
-          const float2 a = SC::pair(sg[p]), b = SC::pair(su[p]);
-          const float gv = wave_sum(a.x * qg + a.y * xsum);
-          const float uv = wave_sum(b.x * qu + b.y * xsum);
-          av[p] = silu(gv) * uv;
-        }
+        F::gate_up(gu, xq4, s_xsum, lane, av);
         if (lane == 0) ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
       }
       ST_MARK(4);
       // down rows (8 experts + shared): issued after the gate_up stores so the gate_up stream
       // has the bandwidth to itself; they land during the activation exchange's first delay
-      const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
-      const uint4 qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
-      const uint4 qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
-      const uint32_t da_s = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
-      const uint32_t db_s = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
+      typename F::DN dn;
+      F::load_dn(Ly, my_idx, n, lane, dn);
       const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
       const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
 
@@ -421,7 +563,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + ST_OFF_ACT);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct<F>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -449,7 +591,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
       // ---- routing weights (s_mz is complete since the activation barrier)
       const float my_w = canon_topk_weight(lg[my_idx], s_mz[0], s_mz[1], ST_TOPK);
       const float sgv = sigmoid(lg[E]);
-      const float wa = __shfl(my_w, ka), wb = __shfl(my_w, 4 + ka);
       if (blockIdx.x == 0 && wave == 0) {
         if (idx_out && lane < ST_TOPK) idx_out[l * ST_TOPK + lane] = my_idx;
         if (wts_out && lane < ST_TOPK) wts_out[l * ST_TOPK + lane] = my_w;
@@ -457,28 +598,16 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
 
       // ---- down row n: 8 experts + shared, weighted, plus the residual
-      float xa[32], xb[32], xc[8];
-      const float suma = s_asum[lane], sumb = s_asum[64 + lane], sumc = s_asum[128 + lane];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float4 v = as4[i * 64 + lane], w = as4[512 + i * 64 + lane];
-        xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
-        xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-      }
+      float xc[8];
+      const float sumc = s_asum[128 + lane];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const float4 v = as4[1024 + i * 64 + lane];
         xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
       }
-      float da = 0.f, db = 0.f;
-      da = dot8_q4(qa.x, xa + 0, da), db = dot8_q4(qb.x, xb + 0, db);
-      da = dot8_q4(qa.y, xa + 8, da), db = dot8_q4(qb.y, xb + 8, db);
-      da = dot8_q4(qa.z, xa + 16, da), db = dot8_q4(qb.z, xb + 16, db);
-      da = dot8_q4(qa.w, xa + 24, da), db = dot8_q4(qb.w, xb + 24, db);
       float dc = dot4_u8b(qs.x, xc, 0.f);
       dc = dot4_u8b(qs.y, xc + 4, dc);
-      const float2 pa = SC::pair(da_s), pb = SC::pair(db_s);
-      float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) + sgv * ssc * (dc - 128.f * sumc);
+      float acc = F::down(dn, as4, s_asum, my_w, lane) + sgv * ssc * (dc - 128.f * sumc);
       acc = wave_sum(acc);
       if (lane == 0) {
         const float y = res + acc;
@@ -490,7 +619,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
-        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + ST_OFF_X);
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + F::kOffX);
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }
@@ -516,15 +645,15 @@ int step_grid_ok(const void* kernel) {
   return ok[dev].load(std::memory_order_relaxed) == 1;
 }
 
-template <class SC, class SH>
+template <class F, class SH>
 int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, int I, int topk, float eps,
                 uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out, float* xs_out,
                 hipStream_t st) {
   if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || L < 1 || L > ST_MAXL) return -1;
   if (!layers || !x || !ll || !sync) return -1;
-  const void* k = reinterpret_cast<const void*>(&k_decode_step<SC, SH>);
+  const void* k = reinterpret_cast<const void*>(&k_decode_step<F, SH>);
   if (!step_grid_ok(k)) return -1;
-  hipLaunchKernelGGL((k_decode_step<SC, SH>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
+  hipLaunchKernelGGL((k_decode_step<F, SH>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
                      idx_out, wts_out, sgate_out, xs_out);
   return 0;
 }
@@ -534,13 +663,27 @@ int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, in
 API int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I, int topk,
                            float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
                            float* xs_out, dr_stream_t st) {
-  return launch_step<ScaleF16, Q8G128F16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+  return launch_step<StepQ4<ScaleF16>, Q8G128F16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
                                           sgate_out, xs_out, (hipStream_t)st);
 }
 
 API int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I,
                                  int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                                  float* sgate_out, float* xs_out, dr_stream_t st) {
-  return launch_step<ScaleBF16, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+  return launch_step<StepQ4<ScaleBF16>, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+                                           sgate_out, xs_out, (hipStream_t)st);
+}
+
+API int dr_moe_decode_step_fp8(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I, int topk,
+                               float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
+                               float* sgate_out, float* xs_out, dr_stream_t st) {
+  return launch_step<StepFP8<0>, Q8G128F16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
+                                           sgate_out, xs_out, (hipStream_t)st);
+}
+
+API int dr_moe_decode_step_fp8_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I,
+                                     int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
+                                     float* sgate_out, float* xs_out, dr_stream_t st) {
+  return launch_step<StepFP8<1>, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, ll, sync, idx_out, wts_out,
                                            sgate_out, xs_out, (hipStream_t)st);
 }

@@ -85,6 +85,15 @@ def q8_dense(rng, N, K, fmt):
     return q, f32_to_bf16(s.astype(np.float32)), BF16, K
 
 
+def fp8_experts_quick(rng, E, N, K, kind):
+    """Like fp8_experts at a fraction of the host time (for large multi-layer tests): codes
+    drawn from a pool of e4m3-rounded N(0, 100) values, block scales |N(0, 0.02)| / 100."""
+    pool = f32_to_e4m3(rng.normal(0, 100.0, size=1 << 16).astype(np.float32))
+    q = pool[rng.integers(0, pool.size, size=(E, N, K), dtype=np.int64)]
+    s = (np.abs(rng.normal(0, 0.02, size=(E, N // 128, K // 128))) + 1e-4).astype(np.float32) / 100.0
+    return np.ascontiguousarray(q), enc(s, kind)
+
+
 def fp8_experts(rng, E, N, K, kind):
     w = rng.normal(0, 0.02, size=(E, N, K)).astype(np.float32)
     blk = w.reshape(E, N // 128, 128, K // 128, 128)
@@ -95,7 +104,7 @@ def fp8_experts(rng, E, N, K, kind):
 
 
 def make_layer(seed: int, E: int = 256, H: int = 2048, I: int = 512, fmt: str = "cfg", kind: str = "q4",
-               with_norm: bool = True) -> dict:
+               with_norm: bool = True, quick: bool = False) -> dict:
     rng = np.random.default_rng(seed)
     L = {"E": E, "H": H, "I": I, "fmt": fmt, "kind": kind}
     L["router"] = f32_to_bf16(rng.normal(0, 0.02, size=(E + 1, H)).astype(np.float32))
@@ -106,8 +115,9 @@ def make_layer(seed: int, E: int = 256, H: int = 2048, I: int = 512, fmt: str = 
         L["d_q"], L["d_s"] = q4_experts(rng, E, H, I, sk)
     else:
         sk = BF16 if fmt == "cfg" else F32
-        L["gu_q"], L["gu_s"] = fp8_experts(rng, E, 2 * I, H, sk)
-        L["d_q"], L["d_s"] = fp8_experts(rng, E, H, I, sk)
+        fx = fp8_experts_quick if quick else fp8_experts
+        L["gu_q"], L["gu_s"] = fx(rng, E, 2 * I, H, sk)
+        L["d_q"], L["d_s"] = fx(rng, E, H, I, sk)
     L["sc_kind"] = sk
     L["sgu_q"], L["sgu_s"], L["sh_kind"], L["sh_group_gu"] = q8_dense(rng, 2 * I, H, fmt)
     L["sd_q"], L["sd_s"], _, L["sh_group_d"] = q8_dense(rng, H, I, fmt)

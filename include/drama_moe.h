@@ -258,6 +258,18 @@ int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, in
 int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                              int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                              float* sgate_out, float* xs_out, dr_stream_t st);
+/* The same step with block-FP8 routed experts: per layer gu_q/d_q are the e4m3 weights and
+ * gu_s/d_s their 128 x 128 block scales of dr_moe_decode_fp8 (f32 scale_inv, int8 shared
+ * scales f16 per 128) or of dr_moe_decode_fp8_bf16s (bf16 block scales, bf16 per-channel
+ * shared scales); everything else as dr_moe_decode_step.  No reference counterpart: the
+ * reference decodes FP8 layers with dr_router_topk + dr_moe_decode_fp8 per layer
+ * (kernels/drama.cu:602-742), which these replace for a whole stack of layers. */
+int dr_moe_decode_step_fp8(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i, int topk,
+                           float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
+                           float* xs_out, dr_stream_t st);
+int dr_moe_decode_step_fp8_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
+                                 int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
+                                 float* sgate_out, float* xs_out, dr_stream_t st);
 
 #ifdef __cplusplus
 }

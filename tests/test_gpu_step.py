@@ -22,11 +22,11 @@ KEYS = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", 
 class Stack:
     """n_layers host layers, their device copies and the device table of dr_decode_layer."""
 
-    def __init__(self, seeds, E, fmt, with_norm=True):
+    def __init__(self, seeds, E, fmt, with_norm=True, kind="q4"):
         import torch
 
-        self.E, self.fmt = E, fmt
-        self.h = [synth.make_layer(s, E=E, fmt=fmt, with_norm=with_norm) for s in seeds]
+        self.E, self.fmt, self.kind = E, fmt, kind
+        self.h = [synth.make_layer(s, E=E, fmt=fmt, with_norm=with_norm, kind=kind, quick=True) for s in seeds]
         self.d = [{k: (dev(L[k]) if L[k] is not None else None) for k in KEYS} for L in self.h]
         tab = np.array([[D.ptr(t[k]) if t[k] is not None else 0 for k in KEYS] for t in self.d], np.uint64)
         self.table = torch.from_numpy(tab.view(np.int64)).to("cuda:0")
@@ -41,7 +41,8 @@ class Stack:
         wts = torch.zeros(n * TOPK, device="cuda")
         sg = torch.zeros(n, device="cuda")
         xs = torch.zeros(n * H, device="cuda")
-        fn = D.lib().dr_moe_decode_step if self.fmt == "ref" else D.lib().dr_moe_decode_step_bf16s
+        name = "dr_moe_decode_step" + ("_fp8" if self.kind == "fp8" else "") + ("" if self.fmt == "ref" else "_bf16s")
+        fn = getattr(D.lib(), name)
         fn(D.ptr(self.table), n, D.ptr(x_dev), self.E, H, I, TOPK, 1e-6, D.ptr(self.ll), D.ptr(self.sync),
            D.ptr(idx) if want_outputs else None, D.ptr(wts) if want_outputs else None,
            D.ptr(sg) if want_outputs else None, D.ptr(xs) if want_outputs else None, D.stream_ptr())
@@ -68,6 +69,18 @@ def test_step_matches_oracle_layer_by_layer(fmt, E, n):
     print(f"step parity fmt={fmt} E={E} layers={n}", flush=True)
     st = Stack([300 + 7 * i for i in range(n)], E, fmt)
     x0 = np.random.default_rng(5).normal(0, 1, H).astype(np.float32)
+    xd = dev(x0)
+    idx, wts, sg, xs = st.run(xd)
+    assert int(host(st.sync)[1]) == 0, "step reported a timeout"
+    check_stack(st, x0, idx, wts, sg, xs, host(xd))
+
+
+@pytest.mark.parametrize("fmt,E,n", [("cfg", 32, 3), ("ref", 16, 2), ("cfg", 8, 2)])
+def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n):
+    """Block-FP8 routed experts (dr_moe_decode_step_fp8*): the same routing and layer bar."""
+    print(f"fp8 step parity fmt={fmt} E={E} layers={n}", flush=True)
+    st = Stack([500 + 3 * i for i in range(n)], E, fmt, kind="fp8")
+    x0 = np.random.default_rng(15).normal(0, 1, H).astype(np.float32)
     xd = dev(x0)
     idx, wts, sg, xs = st.run(xd)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"

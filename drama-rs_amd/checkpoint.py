@@ -139,8 +139,9 @@ class MoeStack:
         """Prefill of loaded layer l for rows token rows (the engine's moe_prefill,
         src/engine.rs:544-604): x f32 [rows, H] residual stream updated in place, hn bf16
         [rows, H] its RMSNorm.  Rows go in chunks of at most `chunk` (grouping handles up to
-        8192 (row, expert) pairs per call): router GEMM, top-k, shared expert, device-side
-        grouping, gather, grouped expert GEMMs and the weighted combine, no host round trip."""
+        8192 (row, expert) pairs per call): router GEMM, top-k, device-side grouping, gather,
+        grouped expert GEMMs and the weighted combine, with the shared expert on a second stream
+        beside them; no host round trip."""
         import ctypes
 
         import torch
@@ -161,17 +162,34 @@ class MoeStack:
         xp, act, yp = z(c * k * H, torch.int16), z(c * k * I, torch.int16), z(c * k * H)
         h = ctypes.c_void_p()
         lib.dr_cublas_create(ctypes.byref(h), st)
+        # the shared expert needs only hn, so it runs on a second stream beside the routing,
+        # grouping and gather and joins before the combine.  Only from a created stream: events
+        # recorded through a wrapper of the null stream (handle 0) did not order the kernels
+        # launched on it (measured: chunk k + 1's shared output overwrote chunk k's before its
+        # combine), so on the null stream everything stays in order on it.
+        overlap = int(st) != 0
+        if overlap:
+            main = torch.cuda.ExternalStream(st)
+            side = torch.cuda.Stream(device=dev)
+            fork, join = torch.cuda.Event(), torch.cuda.Event()
         for r0 in range(0, rows, c):
             n = min(c, rows - r0)
             hr, xr = hn[r0:r0 + n], x[r0:r0 + n]
+            if overlap:
+                fork.record(main)
+                side.wait_event(fork)
+            lib.dr_moe_shared_prefill(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(hr), n, P(sact),
+                                      P(sh), H, I, side.cuda_stream if overlap else st)
+            if overlap:
+                join.record(side)
             lib.dr_gemm(h.value, P(hr), P(L["router"]), P(logits), n, E + 1, H, 0.0)
             lib.dr_moe_topk(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), st)
-            lib.dr_moe_shared_prefill(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(hr), n, P(sact),
-                                      P(sh), H, I, st)
             lib.dr_moe_group(P(idx), n * k, E, P(counts), P(offsets), P(slot_of), st)
             lib.dr_moe_gather_rows(P(slot_of), n, k, P(hr), P(xp), H, st)
             lib.dr_moe_prefill(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(xp), P(offsets), P(counts),
                                P(act), P(yp), E, H, I, st)
+            if overlap:
+                main.wait_event(join)
             lib.dr_moe_combine(P(xr), P(yp), P(slot_of), P(wts), P(sg), P(sh), n, k, H, st)
 
     def chain(self, x, stream=None) -> None:

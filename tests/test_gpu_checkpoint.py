@@ -43,7 +43,8 @@ def test_checkpoint_stack_step_and_chain(tmp_path):
 
 def test_checkpoint_prefill_chunked(tmp_path):
     """MoeStack.prefill over 300 rows: routing bit-exact with the oracle, and chunking (3 chunks
-    of 128 rows) gives the same bits as one 300-row call (rows are independent)."""
+    of 128 rows) gives the same bits as one 300-row call (rows are independent), also with the
+    shared expert overlapped on a second stream."""
     import torch
 
     import synth
@@ -60,6 +61,14 @@ def test_checkpoint_prefill_chunked(tmp_path):
     st.prefill(0, xb.view(rows, H), dhn.view(rows, H), chunk=128)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(host(xa)), bits(host(xb)))
+    # from a created stream the shared expert runs on a second stream beside the routed path
+    xc = dev(x0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        st.prefill(0, xc.view(rows, H), dhn.view(rows, H), chunk=128)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(host(xa)), bits(host(xc)))
     L = layers[0]
     rl = O.router_logits_rows(hn, L["router"], rows, E + 1, H)
     ri, rw, rs = O.moe_topk(rl, rows, E, 8, E + 1)

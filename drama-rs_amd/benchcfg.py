@@ -117,6 +117,10 @@ class Prefill:
 
     def shared_begin(self, lib, L):
         P = D.ptr
+        if self.rows < 64:  # a few rows: the cross-stream events cost more than the overlap saves
+            lib.dr_moe_shared_prefill_bf16s(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(self.hn),
+                                            self.rows, P(self.sact), P(self.sh), H, I, self.sp)
+            return
         self.ev_fork.record(self.st)
         self.st2.wait_event(self.ev_fork)
         lib.dr_moe_shared_prefill_bf16s(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(self.hn), self.rows,
@@ -137,7 +141,8 @@ class Prefill:
         f = lib.dr_moe_prefill_fp8_bf16s if fp8 else lib.dr_moe_prefill_bf16s
         f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.xp), P(self.offsets), P(self.counts), P(self.act),
           P(self.yp), E, H, I, sp)
-        self.st.wait_event(self.ev_join)
+        if self.rows >= 64:
+            self.st.wait_event(self.ev_join)
         lib.dr_moe_combine(P(self.x), P(self.yp), P(self.slot_of), P(self.wts), P(self.sg), P(self.sh), self.rows, TOPK,
                            H, sp)
 

@@ -167,7 +167,7 @@ class MoeStack:
         # recorded through a wrapper of the null stream (handle 0) did not order the kernels
         # launched on it (measured: chunk k + 1's shared output overwrote chunk k's before its
         # combine), so on the null stream everything stays in order on it.
-        overlap = int(st) != 0
+        overlap = int(st) != 0 and c >= 64  # for a few rows the events cost more than they save
         if overlap:
             main = torch.cuda.ExternalStream(st)
             side = torch.cuda.Stream(device=dev)

@@ -231,8 +231,68 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The same canonical GEMM for few rows of A (M <= GR_MAXM, decode batches): one wave per W
+// row, which it loads once and dots with every A row (4 at a time, all loads issued first);
+// 8 waves per block.  Every dot has the canonical order, so C equals k_gemm_canon's bits.
+constexpr int GR_MAXM = 16;
+template <int NCH>
+__global__ void __launch_bounds__(512)
+    k_gemm_rows(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W, float* __restrict__ C, int M,
+                int N, int K, float beta) {
+  const int lane = lane_id();
+  const int n = blockIdx.x * 8 + wave_id();
+  if (n >= N) return;
+  const int KC = K / 8;
+  uint4 w[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + WAVE * j;
+    w[j] = c < KC ? ld16(W + (size_t)n * K + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+  }
+  for (int m0 = 0; m0 < M; m0 += 4) {
+    uint4 av[4][NCH];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + r < M ? m0 + r : M - 1;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + WAVE * j;
+        av[r][j] = c < KC ? ld16(A + (size_t)m * K + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        if (lane + WAVE * j < KC) {
+          const uint4 a = av[r][j], b = w[j];
+          acc = __builtin_fmaf(bf16_lo(b.x), bf16_lo(a.x), acc);
+          acc = __builtin_fmaf(bf16_hi(b.x), bf16_hi(a.x), acc);
+          acc = __builtin_fmaf(bf16_lo(b.y), bf16_lo(a.y), acc);
+          acc = __builtin_fmaf(bf16_hi(b.y), bf16_hi(a.y), acc);
+          acc = __builtin_fmaf(bf16_lo(b.z), bf16_lo(a.z), acc);
+          acc = __builtin_fmaf(bf16_hi(b.z), bf16_hi(a.z), acc);
+          acc = __builtin_fmaf(bf16_lo(b.w), bf16_lo(a.w), acc);
+          acc = __builtin_fmaf(bf16_hi(b.w), bf16_hi(a.w), acc);
+        }
+      }
+      acc = wave_sum(acc);
+      const int m = m0 + r;
+      if (lane == 0 && m < M) {
+        float* c = C + (size_t)m * N + n;
+        *c = beta == 0.f ? acc : acc + beta * *c;
+      }
+    }
+  }
+}
+
 template <int NCH>
 void launch_gemm(const uint16_t* A, const uint16_t* W, float* C, int M, int N, int K, float beta, hipStream_t st) {
+  if (M <= GR_MAXM) {
+    hipLaunchKernelGGL(k_gemm_rows<NCH>, dim3((N + 7) / 8), dim3(512), 0, st, A, W, C, M, N, K, beta);
+    return;
+  }
   const dim3 g((M + 4 * GM_MPW - 1) / (4 * GM_MPW), (N + GM_BN - 1) / GM_BN);
   hipLaunchKernelGGL(k_gemm_canon<NCH>, g, dim3(256), (size_t)GM_BN * (K / 8) * 16, st, A, W, C, M, N, K, beta);
 }

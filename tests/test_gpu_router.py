@@ -101,7 +101,8 @@ def test_moe_topk_rows_bit_exact(rows, E, stride, ties):
     np.testing.assert_array_equal(bits(host(sg)), bits(rs))
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 257, 2048), (5, 33, 512), (17, 64, 4096), (1, 1, 8)])
+@pytest.mark.parametrize("M,N,K", [(300, 257, 2048), (5, 33, 512), (17, 64, 4096), (1, 1, 8), (4, 257, 2048), (16, 257, 2048),
+                                   (8, 100, 4096)])
 def test_gemm_canonical_bit_exact(M, N, K):
     import torch
 

@@ -553,7 +553,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
       ST_MARK(4);
       // down rows (8 experts + shared): issued after the gate_up stores so the gate_up stream
-      // has the bandwidth to itself; they land during the activation exchange's first delay
+      // has the bandwidth to itself, and well before the activation poll, whose reads return
+      // behind them
       typename F::DN dn;
       F::load_dn(Ly, my_idx, n, lane, dn);
       const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);

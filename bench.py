@@ -161,8 +161,10 @@ def main():
         layers = [make_layer_gpu(None, l) for l in range(8)]
         st = torch.cuda.Stream()
         torch.cuda.synchronize()
-        benchcfg.config4_prefill(lib, layers, st)  # warm-up pass (clocks, caches of the code objects)
-        print(json.dumps({"cfg4_prefill_int4": benchcfg.config4_prefill(lib, layers, st)}))
+        # one stream, so that every kernel's trace duration is its own (the default run overlaps
+        # the shared expert with the routing on a second stream)
+        benchcfg.config4_prefill(lib, layers, st, overlap=False)  # warm-up pass (clocks, code objects)
+        print(json.dumps({"cfg4_prefill_int4": benchcfg.config4_prefill(lib, layers, st, overlap=False)}))
         return
     torch.cuda.set_device(0)
     nl = args.layers

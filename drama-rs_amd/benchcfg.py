@@ -95,10 +95,11 @@ def config1_gemv(lib, st, iters=200):
 class Prefill:
     """Buffers of one prefill layer call for `rows` rows (Engine::moe_prefill, src/engine.rs:544-604)."""
 
-    def __init__(self, rows, st):
+    def __init__(self, rows, st, overlap=True):
         z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
         n = rows * TOPK
         self.rows, self.n, self.st, self.sp = rows, n, st, st.cuda_stream
+        self.overlap = overlap and rows >= 64  # for a few rows the cross-stream events cost more than they save
         g = torch.Generator(device="cuda").manual_seed(21)
         self.hn = bf16_bits(torch.randn(rows, H, generator=g, device="cuda"))
         self.x = torch.randn(rows, H, generator=g, device="cuda")
@@ -117,7 +118,7 @@ class Prefill:
 
     def shared_begin(self, lib, L):
         P = D.ptr
-        if self.rows < 64:  # a few rows: the cross-stream events cost more than the overlap saves
+        if not self.overlap:
             lib.dr_moe_shared_prefill_bf16s(P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(self.hn),
                                             self.rows, P(self.sact), P(self.sh), H, I, self.sp)
             return
@@ -141,7 +142,7 @@ class Prefill:
         f = lib.dr_moe_prefill_fp8_bf16s if fp8 else lib.dr_moe_prefill_bf16s
         f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.xp), P(self.offsets), P(self.counts), P(self.act),
           P(self.yp), E, H, I, sp)
-        if self.rows >= 64:
+        if self.overlap:
             self.st.wait_event(self.ev_join)
         lib.dr_moe_combine(P(self.x), P(self.yp), P(self.slot_of), P(self.wts), P(self.sg), P(self.sh), self.rows, TOPK,
                            H, sp)
@@ -160,9 +161,9 @@ class Prefill:
         return hit * per_expert + shared + (L["router"].numel() * 2 if include_router else 0) + acts, hit
 
 
-def config4_prefill(lib, layers, st, iters=40):
+def config4_prefill(lib, layers, st, iters=40, overlap=True):
     """300 token rows, top-8 of 256 (2400 pairs), rotated over the 40 resident layers."""
-    pf = Prefill(300, st)
+    pf = Prefill(300, st, overlap)
     nl = len(layers)
 
     def full(i):
@@ -177,8 +178,9 @@ def config4_prefill(lib, layers, st, iters=40):
     cnt = pf.counts.cpu()
     uniform = rec(ms * 1000, nbytes, experts_hit=hit, rows_per_expert_max=int(cnt.max()), pairs=pf.n,
                   us_graph=round(msg * 1000, 2),
-                  note="router GEMM + top-k + group + gather + grouped GEMM + combine, the shared expert on a second "
-                       "stream beside them; us_graph: replayed from a HIP graph")
+                  note="router GEMM + top-k + group + gather + grouped GEMM + combine" + (
+                      ", the shared expert on a second stream beside them" if pf.overlap else " + shared, one stream")
+                       + "; us_graph: replayed from a HIP graph")
     # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
     g = torch.Generator(device="cuda").manual_seed(31)
     hot = torch.randperm(E, generator=g, device="cuda")[: E // 10]

@@ -7,6 +7,9 @@
 // staged once per block through LDS with a lane-major swizzle.  int8 values enter the fp32 FMA
 // as (byte ^ 0x80) via v_cvt_f32_ubyte, with 128 * sum(x) subtracted once per chunk.
 // K = 512 rows are 8 bytes per lane.
+#include <algorithm>
+#include <atomic>
+
 #include "common.hpp"
 
 using namespace drm;
@@ -50,13 +53,16 @@ DEV void stage_x_lanes(const float* __restrict__ x, const float* __restrict__ nw
   __syncthreads();
 }
 
-// int8 row dot over CPL 16-byte chunks per lane (K = 1024 CPL); S: scale functor
-template <int CPL, class SCL>
-DEV float row_dot_q8(const int8_t* __restrict__ row, const float (*xv)[16], const float* xsum, SCL scl) {
+// int8 row dot over CPL 16-byte chunks per lane (K = 1024 CPL), from the lane's loaded chunks
+// w (load_q8); S: scale functor
+template <int CPL>
+DEV void load_q8(const int8_t* __restrict__ row, uint4 (&w)[CPL]) {
   const int lane = lane_id();
-  uint4 w[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) w[j] = ld16(row + (size_t)(lane + 64 * j) * 16);
+}
+template <int CPL, class SCL>
+DEV float row_dot_q8(const uint4 (&w)[CPL], const float (*xv)[16], const float* xsum, SCL scl) {
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -70,13 +76,29 @@ DEV float row_dot_q8(const int8_t* __restrict__ row, const float (*xv)[16], cons
 }
 
 // MODE 0: y = W xn (+ res);  MODE 1: swiglu pair rows;  SK 0: f16 per 128 (reference), 1: bf16 per row
-template <int CPL, int MODE, int SK>
+template <int CPL, int MODE, int SK, bool PRE_OK>
 __global__ void __launch_bounds__(GV8_WPB * 64)
     k_gemv_q8(const int8_t* __restrict__ W, const uint16_t* __restrict__ S, const float* __restrict__ x, const float* res,
               float* y, int N, const float* __restrict__ nw, float eps, const char* pf, size_t pf_bytes) {
   constexpr int K = 1024 * CPL;
+  constexpr int NR = MODE == 1 ? 2 : 1;  // rows per output: the gate and up rows of a pair
   __shared__ float4 xs[K / 4];
   const int lane = lane_id(), wave = wave_id();
+  const int row0 = (blockIdx.x * GV8_WPB + wave) * GV8_RPW;
+  // PRE_OK (small N, where a block's latency is not hidden by other blocks): every weight load
+  // of the wave first, so they stream while x is staged (up to 4 chunks per row and lane);
+  // otherwise each row loads before its dot and more blocks fit on a CU
+  constexpr bool PRE = PRE_OK && CPL * NR <= 4;
+  uint4 w[GV8_RPW][NR][CPL];
+  auto load_row = [&](int r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+#pragma unroll
+    for (int h = 0; h < NR; ++h) load_q8<CPL>(W + (size_t)(n + h * N) * K, w[r][h]);
+  };
+  if constexpr (PRE) {
+#pragma unroll
+    for (int r = 0; r < GV8_RPW; ++r) load_row(r);
+  }
   stage_x_lanes<16>(x, nw, eps, K, xs);
   float xv[CPL][16], xsum[CPL];
 #pragma unroll
@@ -89,12 +111,11 @@ __global__ void __launch_bounds__(GV8_WPB * 64)
       xsum[j] += (v.x + v.y) + (v.z + v.w);
     }
   }
-  const int rows_out = MODE == 1 ? N : N;
-  const int row0 = (blockIdx.x * GV8_WPB + wave) * GV8_RPW;
 #pragma unroll
   for (int r = 0; r < GV8_RPW; ++r) {
     const int n = row0 + r;
-    if (n >= rows_out) break;
+    if (n >= N) break;
+    if constexpr (!PRE) load_row(r);
     auto scl_of = [&](size_t row) {
       return [=](int j) {
         if (SK == 1) return bf16f(S[row]);
@@ -102,13 +123,75 @@ __global__ void __launch_bounds__(GV8_WPB * 64)
       };
     };
     if (MODE == 0) {
-      float d = wave_sum(row_dot_q8<CPL>(W + (size_t)n * K, xv, xsum, scl_of((size_t)n)));
+      float d = wave_sum(row_dot_q8<CPL>(w[r][0], xv, xsum, scl_of((size_t)n)));
       if (lane == 0) y[n] = d + (res ? res[n] : 0.f);
     } else {
-      const float g = wave_sum(row_dot_q8<CPL>(W + (size_t)n * K, xv, xsum, scl_of((size_t)n)));
-      const float u = wave_sum(row_dot_q8<CPL>(W + (size_t)(N + n) * K, xv, xsum, scl_of((size_t)(N + n))));
+      const float g = wave_sum(row_dot_q8<CPL>(w[r][0], xv, xsum, scl_of((size_t)n)));
+      const float u = wave_sum(row_dot_q8<CPL>(w[r][NR - 1], xv, xsum, scl_of((size_t)(N + n))));
       if (lane == 0) y[n] = silu(g) * u;
     }
+  }
+  warm_range(pf, pf_bytes);
+}
+
+// Large-N form of MODE 0 (the lm_head): a grid of GV8_PB blocks per CU stages x once and each
+// wave walks tiles of GV8_RPW rows spaced by the grid, the next tile's loads issued before the
+// current tile's dots (two tiles of weight chunks in registers).  Same arithmetic per row as
+// k_gemv_q8.
+constexpr int GV8_PB = 4;  // measured: 2 -> 51.0 us, 3 -> 55, 4 -> 50.5 (lm_head 151936 x 2048)
+template <int CPL, int SK>
+__global__ void __launch_bounds__(GV8_WPB * 64)
+    k_gemv_q8_walk(const int8_t* __restrict__ W, const uint16_t* __restrict__ S, const float* __restrict__ x,
+                   const float* res, float* y, int N, const float* __restrict__ nw, float eps, const char* pf,
+                   size_t pf_bytes) {
+  constexpr int K = 1024 * CPL;
+  __shared__ float4 xs[K / 4];
+  const int lane = lane_id(), wave = wave_id();
+  // tiles of GV8_RPW rows, wave after wave, spaced by the grid (waves running side by side
+  // read neighbouring rows: measured faster than a contiguous share per wave)
+  const int step = gridDim.x * GV8_WPB * GV8_RPW, end = N;
+  int base = (blockIdx.x * GV8_WPB + wave) * GV8_RPW;
+  uint4 w[2][GV8_RPW][CPL];
+  auto load_tile = [&](int b, uint4 (&tl)[GV8_RPW][CPL]) {
+#pragma unroll
+    for (int r = 0; r < GV8_RPW; ++r) {
+      const int n = b + r < end ? b + r : end - 1;
+      load_q8<CPL>(W + (size_t)n * K, tl[r]);
+    }
+  };
+  if (base < end) load_tile(base, w[0]);
+  stage_x_lanes<16>(x, nw, eps, K, xs);
+  float xv[CPL][16], xsum[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    xsum[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = xs[j * 256 + i * 64 + lane];
+      xv[j][4 * i] = v.x, xv[j][4 * i + 1] = v.y, xv[j][4 * i + 2] = v.z, xv[j][4 * i + 3] = v.w;
+      xsum[j] += (v.x + v.y) + (v.z + v.w);
+    }
+  }
+  auto dots = [&](int b, const uint4 (&tl)[GV8_RPW][CPL]) {
+#pragma unroll
+    for (int r = 0; r < GV8_RPW; ++r) {
+      const int n = b + r;
+      if (n >= end) break;
+      const float d = wave_sum(row_dot_q8<CPL>(tl[r], xv, xsum, [&](int j) {
+        if (SK == 1) return bf16f(S[n]);
+        return f16f(S[(size_t)n * (K / 128) + (size_t)((lane + 64 * j) * 16) / 128]);
+      }));
+      if (lane == 0) y[n] = d + (res ? res[n] : 0.f);
+    }
+  };
+  for (; base < end; base += step) {
+    // two register tiles alternate; the loop is unrolled by hand so both stay in registers
+    if (base + step < end) load_tile(base + step, w[1]);
+    dots(base, w[0]);
+    base += step;
+    if (base >= end) break;
+    if (base + step < end) load_tile(base + step, w[0]);
+    dots(base, w[1]);
   }
   warm_range(pf, pf_bytes);
 }
@@ -198,12 +281,32 @@ int launch_q8(const int8_t* W, const uint16_t* S, const float* x, const float* r
               const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st) {
   if (N <= 0) return N == 0 ? 0 : -1;
   const dim3 g(blocks_for(N)), b(GV8_WPB * 64);
+  const bool small = N <= 16384;  // at most ~2 blocks per CU
+  if (MODE == 0 && !small && (K == 1024 || K == 2048)) {
+    static std::atomic<int> cus{0};
+    if (cus.load(std::memory_order_relaxed) == 0) {
+      int dev = 0, c = 0;
+      (void)hipGetDevice(&dev);
+      (void)hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+      cus.store(c > 0 ? c : 256, std::memory_order_relaxed);
+    }
+    const dim3 gw(std::min<int>(blocks_for(N), GV8_PB * cus.load(std::memory_order_relaxed)));
+    if (K == 1024) hipLaunchKernelGGL((k_gemv_q8_walk<1, SK>), gw, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+    else hipLaunchKernelGGL((k_gemv_q8_walk<2, SK>), gw, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+    return 0;
+  }
   switch (K) {
     case 512: hipLaunchKernelGGL((k_gemv_q8_k512<MODE, SK>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
-    case 1024: hipLaunchKernelGGL((k_gemv_q8<1, MODE, SK>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
-    case 2048: hipLaunchKernelGGL((k_gemv_q8<2, MODE, SK>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
-    case 4096: hipLaunchKernelGGL((k_gemv_q8<4, MODE, SK>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
-    case 6144: hipLaunchKernelGGL((k_gemv_q8<6, MODE, SK>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
+    case 1024: if (small) hipLaunchKernelGGL((k_gemv_q8<1, MODE, SK, true>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      else hipLaunchKernelGGL((k_gemv_q8<1, MODE, SK, false>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      break;
+    case 2048: if (small) hipLaunchKernelGGL((k_gemv_q8<2, MODE, SK, true>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      else hipLaunchKernelGGL((k_gemv_q8<2, MODE, SK, false>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      break;
+    case 4096: if (small) hipLaunchKernelGGL((k_gemv_q8<4, MODE, SK, true>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      else hipLaunchKernelGGL((k_gemv_q8<4, MODE, SK, false>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes);
+      break;
+    case 6144: hipLaunchKernelGGL((k_gemv_q8<6, MODE, SK, false>), g, b, 0, st, W, S, x, res, y, N, nw, eps, pf, pf_bytes); break;
     default: return -1;
   }
   return 0;

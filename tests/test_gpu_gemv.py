@@ -25,12 +25,12 @@ def xn_of(x, nw):
     return O.rmsnorm(x, nw, 1e-6) if nw is not None else x
 
 
-@pytest.mark.parametrize("K", [512, 2048, 4096, 6144])
+@pytest.mark.parametrize("K,N", [(512, 1000), (2048, 1000), (4096, 1000), (6144, 1000), (1024, 17001), (2048, 20003)])
 @pytest.mark.parametrize("with_norm", [True, False])
-def test_gemv_q8(K, with_norm):
+def test_gemv_q8(K, N, with_norm):
+    """Above 16384 rows the K = 1024 / 2048 forms walk row tiles with a grid of 2 blocks per CU."""
     import torch
 
-    N = 1000
     q, s, kind, group, x, nw, res = q8_case(K, N, K, "ref")
     nw = nw if with_norm else None
     ref = O.gemv_q8(q, s, kind, group, xn_of(x, nw), N, K) + res

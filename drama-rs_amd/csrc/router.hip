@@ -112,8 +112,8 @@ __global__ void __launch_bounds__(RT_WPB * 64)
 }
 
 // One row per block.  topk <= 8: waves 0..3 each pick the top 8 of 64 experts and wave 4
-// computes the softmax denominator, then wave 0 merges the 32 candidates (the same selection
-// and weights as canon_softmax_topk, in about half the time); topk > 8: wave 0 alone.
+// computes the softmax denominator, then wave 0 ranks the 32 candidates (the same selection
+// and weights as canon_softmax_topk, in less than half the time); topk > 8: wave 0 alone.
 __global__ void __launch_bounds__(320)
     k_moe_topk(const float* __restrict__ logits, int E, int topk, int stride, int* __restrict__ idx,
                float* __restrict__ wts, float* __restrict__ sgate) {

@@ -50,7 +50,7 @@ constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the
 // polls slow the exchange for everybody; these offsets were measured on MI355X
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
-constexpr uint32_t ST_OFF_LOGITS = 185, ST_DLY_ROUND = 20;  // the other two offsets depend on the format
+constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll offsets are per format
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
@@ -209,7 +209,7 @@ struct SpecAct {
 template <class SC>
 struct StepQ4 {
   static constexpr bool kMinTerm = true;
-  static constexpr uint32_t kOffAct = 370, kOffX = 285;  // first-poll offsets (measured)
+  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 285;  // first-poll offsets (measured)
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -293,7 +293,7 @@ struct StepQ4 {
 template <int SF>
 struct StepFP8 {
   static constexpr bool kMinTerm = false;
-  static constexpr uint32_t kOffAct = 430, kOffX = 245;  // twice the gate_up bytes of int4 (measured)
+  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 245;  // twice the gate_up bytes of int4 (measured)
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];
@@ -505,7 +505,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(1);
     }
     if (poller) {
-      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, t_layer + ST_OFF_LOGITS);
+      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, t_layer + F::kOffL);
       if (!r && lane == 0) s_abort = 1;
       ST_PUT(8, r);
     }

@@ -47,7 +47,8 @@ constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the
 // like the non-router waves at the logits, do not poll before the data can be there): the
 // logits after the layer start, the activations after top-k, the residual after the
 // activation barrier.  A poll that comes too early costs a whole extra round trip, and early
-// polls slow the exchange for everybody; these offsets were measured on MI355X
+// polls slow the exchange for everybody; the offsets (kOffL, kOffAct, kOffX of the weight-format
+// policies below) were measured on MI355X
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
 constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll offsets are per format

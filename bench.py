@@ -140,7 +140,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is a design "
-              "note (DESIGN.md), not a measured configuration", file=sys.stderr)
+              "note, not a measured configuration", file=sys.stderr)
         sys.exit(2)
     import torch
 

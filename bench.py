@@ -39,6 +39,8 @@ def parse():
                          "the run that rocprofv3 --pmc / --kernel-trace profiles")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="only configuration 4 (prefill, 8 resident layers): the run profiled for the grouped GEMM")
+    ap.add_argument("--profile-fp8", action="store_true",
+                    help="only configuration 5 (FP8 decode, batch 1 and 4, int8 lm_head): the run profiled for its kernels")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only a 1 GiB device-to-device copy, 5 times: calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
@@ -165,6 +167,12 @@ def main():
         # the shared expert with the routing on a second stream)
         benchcfg.config4_prefill(lib, layers, st, overlap=False)  # warm-up pass (clocks, code objects)
         print(json.dumps({"cfg4_prefill_int4": benchcfg.config4_prefill(lib, layers, st, overlap=False)}))
+        return
+    if args.profile_fp8:
+        import benchcfg
+
+        st = torch.cuda.Stream()
+        print(json.dumps({"cfg5_fp8_and_int8": benchcfg.config5_fp8(lib, st)}))
         return
     torch.cuda.set_device(0)
     nl = args.layers

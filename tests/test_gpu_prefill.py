@@ -74,12 +74,14 @@ def test_group_exact(n, E, skew):
         np.testing.assert_array_equal(host(slot_of)[:n], rs)
 
 
-def test_count_and_permute_reference_abi():
-    """dr_moe_count + host scan + dr_moe_permute, the reference's sequence (src/engine.rs:564-578)."""
+@pytest.mark.parametrize("rows", [300, 4, 8, 9])
+def test_count_and_permute_reference_abi(rows):
+    """dr_moe_count + host scan + dr_moe_permute, the reference's sequence (src/engine.rs:564-578),
+    at prefill and decode-batch row counts."""
     import torch
 
-    rng = np.random.default_rng(3)
-    rows, topk, E = 300, 8, 256
+    rng = np.random.default_rng(3 + rows)
+    topk, E = 8, 256
     idx = rng.integers(0, E, rows * topk).astype(np.int32)
     x = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
     rc, ro, rs = O.moe_group(idx, E)

@@ -101,6 +101,41 @@ def test_moe_topk_rows_bit_exact(rows, E, stride, ties):
     np.testing.assert_array_equal(bits(host(sg)), bits(rs))
 
 
+def test_moe_topk_special_values():
+    """Prefill top-k on logits holding signed zeros, infinities and NaNs (-0 just below +0,
+    NaN last, lowest index on ties): indices bit-exact with the oracle; weights and shared
+    gates bit-exact where the oracle's are finite, NaN where its are NaN."""
+    import torch
+
+    rows, E, stride = 6, 64, 65
+    rng = np.random.default_rng(11)
+    lg = rng.normal(0, 1, (rows, stride)).astype(np.float32)
+    lg[0, :] = -1.0
+    lg[0, [3, 9, 17, 30]] = 0.0
+    lg[0, [5, 12, 40, 41, 60]] = -0.0  # the 8th pick falls among the -0s: lowest indices win
+    lg[1, [2, 7]] = np.inf
+    lg[2, :E:3] = np.nan
+    lg[3, :] = -np.inf
+    lg[3, [4, 44]] = 1.0
+    lg[4, : E - 4] = np.nan  # fewer than 8 ordered values
+    lg[5, :] = 0.5  # all equal
+    lg[:, E] = rng.normal(0, 1, rows).astype(np.float32)  # shared gate logit
+    lg[1, E] = -np.inf
+    ri, rw, rs = O.moe_topk(lg, rows, E, 8, stride)
+    idx = torch.empty(rows * 8, dtype=torch.int32, device="cuda")
+    wts = torch.empty(rows * 8, dtype=torch.float32, device="cuda")
+    sg = torch.empty(rows, dtype=torch.float32, device="cuda")
+    D.lib().dr_moe_topk(D.ptr(dev(lg)), rows, E, 8, stride, D.ptr(idx), D.ptr(wts), D.ptr(sg), D.stream_ptr())
+    torch.cuda.synchronize()
+    hi, hw, hs = host(idx), host(wts), host(sg)
+    np.testing.assert_array_equal(hi, ri)
+    assert ((hi >= 0) & (hi < E)).all()
+    for got, ref in ((hw, rw), (hs, rs)):
+        fin = np.isfinite(ref)
+        np.testing.assert_array_equal(bits(got[fin]), bits(ref[fin]))
+        np.testing.assert_array_equal(np.isnan(got[~fin]), np.isnan(ref[~fin]))
+
+
 @pytest.mark.parametrize("M,N,K", [(300, 257, 2048), (5, 33, 512), (17, 64, 4096), (1, 1, 8), (4, 257, 2048), (16, 257, 2048),
                                    (8, 100, 4096)])
 def test_gemm_canonical_bit_exact(M, N, K):

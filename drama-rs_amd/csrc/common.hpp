@@ -14,6 +14,19 @@ namespace drm {
 
 constexpr int WAVE = 64;
 
+// Library error word: one host-mapped pinned word shared by every device, written by a kernel
+// whose bounded wait gave up (system-scope store) and read by the host without synchronising
+// (dr_last_error, dr_stream_sync, the launchers).  err_word() returns its device address,
+// nullptr if it could not be set up; err_pending() the current code (0 = none).
+// Codes (the header's DR_ERR_STEP_TIMEOUT / DR_ERR_PREFILL_WAIT).
+constexpr uint32_t kErrStepTimeout = 9001, kErrPrefillWait = 9002;
+uint32_t* err_word();
+uint32_t err_pending();
+
+DEV void raise_err(uint32_t* err, uint32_t code) {
+  if (err) __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 DEV float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
 DEV float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 DEV float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }

@@ -31,7 +31,8 @@ DEV uint64_t match8(uint32_t key, bool valid) {
   return m;
 }
 
-// mode 0: compute counts/offsets and slots; mode 1: offsets given (dr_moe_permute), also fill
+// mode 0: compute counts/offsets and slots; mode 1 (dr_moe_permute): offsets given, fill holds
+// the pairs of each expert already placed by earlier segments and is advanced by this one
 __global__ void __launch_bounds__(GR_THREADS)
     k_group(const int* __restrict__ idx, int n, int E, int* __restrict__ counts, int* __restrict__ offsets,
             int* __restrict__ slot_of, int mode, int* __restrict__ fill) {
@@ -88,11 +89,15 @@ __global__ void __launch_bounds__(GR_THREADS)
     int base = 0;
     for (int w = 0; w < wave; ++w) base += s_wsum[w];
     const int e = threadIdx.x;
-    const int off = mode == 0 ? s_off[e] + base : offsets[e];
-    s_off[e] = off;
-    if (e < E) {
-      if (mode == 0) counts[e] = total, offsets[e] = off;
-      else fill[e] = total;
+    if (mode == 0) {
+      s_off[e] = s_off[e] + base;
+      if (e < E) counts[e] = total, offsets[e] = s_off[e];
+    } else if (total > 0) {
+      // only experts that occur in this segment are touched (offsets/fill have the caller's E
+      // entries); fill carries the pairs of earlier segments, so slots stay stable across them
+      const int f = fill[e];
+      s_off[e] = offsets[e] + f;
+      fill[e] = f + total;
     }
   }
   __syncthreads();
@@ -190,11 +195,17 @@ API int dr_moe_count(const int* idx, int n, int* counts, hipStream_t st) {
 
 API int dr_moe_permute(const int* idx, int rows, int topk, const int* offsets, int* fill, int* slot_of,
                        const uint16_t* x, uint16_t* xp, int H, hipStream_t st) {
-  const int n = rows * topk;
-  if (n < 0 || n > GR_MAXN || H % 8 != 0 || topk < 1) return -1;
+  if (rows < 0 || topk < 1 || H % 8 != 0) return -1;
+  const long long nl = (long long)rows * topk;
+  if (nl > (1ll << 30)) return -1;
+  const int n = (int)nl;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, 256, nullptr, const_cast<int*>(offsets),
-                     slot_of, 1, fill);
+  // segments of GR_MAXN pairs in stream order; fill (zero on entry) is the running base
+  for (int s0 = 0; s0 < n; s0 += GR_MAXN) {
+    const int m = n - s0 < GR_MAXN ? n - s0 : GR_MAXN;
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx + s0, m, 256, nullptr,
+                       const_cast<int*>(offsets), slot_of + s0, 1, fill);
+  }
   hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(256), 0, st, slot_of, topk, x, xp, H);
   return 0;
 }

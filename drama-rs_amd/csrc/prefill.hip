@@ -148,12 +148,14 @@ struct Raw<FmtFP8<SF>> {
 };
 
 // Spin until an LDS counter reaches target (acquire); bounded, so a broken protocol ends the
-// wait instead of hanging the GPU (the results are then wrong, which the tests catch).
-DEV void lds_wait_ge(const uint32_t* c, uint32_t target) {
+// wait instead of hanging the GPU, and then raises DR_ERR_PREFILL_WAIT in the library error
+// word (the results of the launch are wrong; dr_stream_sync and dr_last_error report it).
+DEV void lds_wait_ge(const uint32_t* c, uint32_t target, uint32_t* err) {
   for (int it = 0; it < (1 << 22); ++it) {
     if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
     __builtin_amdgcn_s_sleep(1);
   }
+  if (lane_id() == 0) raise_err(err, kErrPrefillWait);
 }
 DEV void lds_count(uint32_t* c) {
   if (lane_id() == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -262,7 +264,7 @@ template <class F, int MODE, int K>
 __global__ void __launch_bounds__(PF_GWPB * 64)
     k_grouped(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
               const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
-              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int E) {
+              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int E, uint32_t* __restrict__ err) {
   extern __shared__ uint4 xs[];  // two tile buffers of BUF blocks, the item table, the up hand-over
   constexpr int BUF = PF_TOK * K / 8 + (F::paired ? (K / 64) * PF_TOK / 4 : 0);
   constexpr int WR = MODE == 0 ? PF_GWPB / 2 : PF_GWPB;  // row tiles per item (per row set)
@@ -415,7 +417,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   } pend;
   pend.valid = false;
   auto finish_gate = [&](const Pending& pd, int k1) {
-    lds_wait_ge(&n_up, (uint32_t)(WR * (k1 + 1)));
+    lds_wait_ge(&n_up, (uint32_t)(WR * (k1 + 1)), err);
 #pragma unroll
     for (int t = 0; t < PF_GRPW; ++t) {
       const f32x4 u = ups[(((k1 & 1) * PF_GRPW + t) * WR + wt) * 64 + lane];
@@ -527,7 +529,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
       }
       __builtin_amdgcn_sched_barrier(0);
       if (i == (NS == 2 ? 1 : NS / 2 - 1)) {  // measured: step 3 of 8 (1, 2 and 5 slower)
-        lds_wait_ge(&n_done, (uint32_t)(PF_GWPB * k));
+        lds_wait_ge(&n_done, (uint32_t)(PF_GWPB * k), err);
         tt.store(xs + ((k + 1) & 1) * BUF, F::paired);
         lds_count(&n_stored);
         __builtin_amdgcn_sched_barrier(0);
@@ -549,7 +551,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
         }
       } else if (up) {
         // ups[k & 1] held item k - 2, which every gate wave has read
-        lds_wait_ge(&n_gate, (uint32_t)(WR * (k > 0 ? k - 1 : 0)));
+        lds_wait_ge(&n_gate, (uint32_t)(WR * (k > 0 ? k - 1 : 0)), err);
         ups[(((k & 1) * PF_GRPW + t) * WR + wt) * 64 + lane] = tA;
         lds_count(&n_up);
       } else {
@@ -563,7 +565,7 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     cur = nxt;
     nxt = item_at(blockIdx.x + (k + 2) * gridDim.x);
     // the next tile is complete once every wave stored its part
-    lds_wait_ge(&n_stored, (uint32_t)(PF_GWPB * (k + 1)));
+    lds_wait_ge(&n_stored, (uint32_t)(PF_GWPB * (k + 1)), err);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (MODE == 0 && !up && pend.valid) finish_gate(pend, k);  // the last item
@@ -883,7 +885,8 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
                      (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0) + (F::paired ? (size_t)K * 2 : 0);
   auto kern = mode == 0 ? k_grouped<F, 0, 2048> : k_grouped<F, 1, 512>;
   int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E,
+                     err_word());
 }
 
 // gate_up then down for all experts of a grouped batch

@@ -2,16 +2,62 @@
 // Thin HIP calls; the engine never needs HIP headers.
 #include "common.hpp"
 
+#include <cstring>
+#include <mutex>
 #include <new>
 
 using namespace drm;
 
+namespace {
+// The error word lives in pinned, mapped host memory (portable to every device), so kernels on
+// any GPU can set it and the host reads it with a plain load.  Set up once per process.
+uint32_t* g_err_host = nullptr;
+uint32_t* g_err_dev = nullptr;
+std::once_flag g_err_once;
+
+void err_setup() {
+  void* p = nullptr;
+  if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  std::memset(p, 0, 64);
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  g_err_host = static_cast<uint32_t*>(p);
+  g_err_dev = static_cast<uint32_t*>(d);
+}
+}  // namespace
+
+uint32_t* drm::err_word() {
+  std::call_once(g_err_once, err_setup);
+  return g_err_dev;
+}
+uint32_t drm::err_pending() {
+  return g_err_host ? __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) : 0u;
+}
+
 API const char* dr_error_string(int e) {
   if (e == -1) return "unsupported shape";
+  if (e == (int)kErrStepTimeout)
+    return "fused decode step gave up waiting for its workgroups (not co-resident: another kernel held CUs)";
+  if (e == (int)kErrPrefillWait) return "prefill grouped GEMM gave up waiting for an LDS hand-off";
   return hipGetErrorString((hipError_t)e);
 }
-API int dr_last_error(void) { return (int)hipGetLastError(); }
-API int dr_malloc(void** p, size_t n) { return (int)hipMalloc(p, n); }
+// The runtime's last launch error first; then a pending library error, which this call clears.
+API int dr_last_error(void) {
+  const int e = (int)hipGetLastError();
+  if (e) return e;
+  if (!g_err_host) return 0;
+  return (int)__atomic_exchange_n(g_err_host, 0u, __ATOMIC_ACQ_REL);
+}
+API int dr_malloc(void** p, size_t n) {
+  (void)err_word();
+  return (int)hipMalloc(p, n);
+}
 API int dr_free(void* p) { return (int)hipFree(p); }
 API int dr_host_alloc(void** p, size_t n) { return (int)hipHostMalloc(p, n, hipHostMallocDefault); }
 API int dr_host_free(void* p) { return (int)hipHostFree(p); }
@@ -45,8 +91,15 @@ API int dr_memset(void* d, int v, size_t n, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-API int dr_stream_create(hipStream_t* s) { return (int)hipStreamCreateWithFlags(s, hipStreamNonBlocking); }
-API int dr_stream_sync(hipStream_t s) { return (int)hipStreamSynchronize(s); }
+API int dr_stream_create(hipStream_t* s) {
+  (void)err_word();  // set the error word up now, outside any graph capture
+  return (int)hipStreamCreateWithFlags(s, hipStreamNonBlocking);
+}
+// A pending library error (left for dr_last_error to clear) is reported after the wait.
+API int dr_stream_sync(hipStream_t s) {
+  const int e = (int)hipStreamSynchronize(s);
+  return e ? e : (int)err_pending();
+}
 API int dr_device_sync(void) { return (int)hipDeviceSynchronize(); }
 API int dr_mem_info(size_t* free_b, size_t* total_b) { return (int)hipMemGetInfo(free_b, total_b); }
 

@@ -52,11 +52,12 @@ constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
 constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll offsets are per format
-constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // s_memrealtime runs at 100 MHz: 0.2 s
+constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
 constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + (ST_TOPK + 1) * ST_I, LL_WORDS = LL_X + ST_H;
 static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
+static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT, "error codes");
 
 // Phase timestamps for development builds (-DST_TRACE): thread 0 of each block stores the
 // 100 MHz clock at points 0..7 and 11..14 of each layer (poll rounds at 8..10, 15) into
@@ -109,7 +110,8 @@ DEV int slot_q4(int f) { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
 // whose tag is not yet the phase's until all are current, then hands each to spec.store.  Returns the rounds taken, 0 after ~0.2 s (the
 // caller aborts).
 template <int N, int NP, class Spec>
-DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync, uint64_t first_poll) {
+DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sync, uint64_t first_poll,
+                       uint64_t tmo) {
   const int lane = lane_id();
   wait_until(first_poll);
   const uint64_t* b = base + lane + 64 * p;
@@ -126,7 +128,7 @@ DEV uint32_t poll_wave(const uint64_t* base, int p, const Spec& sp, uint32_t* sy
 #pragma unroll
     for (int i = 0; i < N; ++i) good &= sp.ok(p + NP * i, v[i]);
     if (__ballot(!good) == 0) break;
-    if ((it & 63) == 0 && __builtin_amdgcn_s_memrealtime() - t0 > ST_TIMEOUT_TICKS) {
+    if ((it & 63) == 0 && __builtin_amdgcn_s_memrealtime() - t0 > tmo) {
       if (lane == 0) __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return 0;
     }
@@ -388,7 +390,8 @@ template <class F, class SH>
 __global__ void __launch_bounds__(ST_NT, 1)
     k_decode_step(const dr_decode_layer* __restrict__ layers, int L, float* x, int E, float eps,
                   uint64_t* __restrict__ ll, uint32_t* __restrict__ sync, int* __restrict__ idx_out,
-                  float* __restrict__ wts_out, float* __restrict__ sgate_out, float* __restrict__ xs_out) {
+                  float* __restrict__ wts_out, float* __restrict__ sgate_out, float* __restrict__ xs_out,
+                  uint32_t* __restrict__ err, uint64_t tmo) {
   constexpr int H = ST_H, I = ST_I;
   __shared__ float4 xr4[H / 4];                        // residual stream x (raw)
   __shared__ float4 nws[H / 4];                        // RMSNorm weight of the layer
@@ -402,8 +405,19 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float s_mz[2];
   __shared__ int s_abort;
   __shared__ dr_decode_layer s_tab[ST_TABL];  // the first ST_TABL layer records
-  if (__syncthreads_or(__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) return;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  // A block that gives up (a bounded wait expired, or an earlier call did and sync was not
+  // reset) poisons the whole output with NaN and raises DR_ERR_STEP_TIMEOUT, so a failed call
+  // can never pass for a result.
+  auto give_up = [&]() {
+    const float q = __builtin_nanf("");
+    reinterpret_cast<float4*>(x)[tid] = make_float4(q, q, q, q);
+    if (tid == 0) raise_err(err, kErrStepTimeout);
+  };
+  if (__syncthreads_or(__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
+    give_up();
+    return;
+  }
   const int pw = wave;  // every wave polls rows pw + 8 i of each exchange
   const bool poller = true;
   const int g = blockIdx.x * ST_WPB + wave;
@@ -506,7 +520,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(1);
     }
     if (poller) {
-      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, t_layer + F::kOffL);
+      const uint32_t r = poll_wave<1, ST_NP>(ll + LL_LOG, pw, Spec32{tA, E + 1, lg}, sync, t_layer + F::kOffL, tmo);
       if (!r && lane == 0) s_abort = 1;
       ST_PUT(8, r);
     }
@@ -519,7 +533,10 @@ __global__ void __launch_bounds__(ST_NT, 1)
     }
     __syncthreads();
     ST_MARK(2);
-    if (s_abort) return;
+    if (s_abort) {
+      give_up();
+      return;
+    }
 
     // ---- top-k, second half: the 32 candidates ranked by every wave (no second barrier);
     // lane k < 8 of each wave's s_sel row receives pick k
@@ -565,7 +582,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct<F>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct);
+        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct<F>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct, tmo);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -575,7 +592,10 @@ __global__ void __launch_bounds__(ST_NT, 1)
       __syncthreads();
       ST_MARK(5);
       const uint64_t t_act = __builtin_amdgcn_s_memrealtime();
-      if (s_abort) return;
+      if (s_abort) {
+      give_up();
+      return;
+    }
 
       // ---- next layer's known weights: issued after the activation poll (a wave's loads
       // return in order, so loads issued before a poll would delay it)
@@ -621,14 +641,17 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
-        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + F::kOffX);
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + F::kOffX, tmo);
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }
     }
     __syncthreads();
     ST_MARK(7);
-    if (s_abort) return;
+    if (s_abort) {
+      give_up();
+      return;
+    }
   }
   if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -647,6 +670,8 @@ int step_grid_ok(const void* kernel) {
   return ok[dev].load(std::memory_order_relaxed) == 1;
 }
 
+std::atomic<uint64_t> g_wait_ticks{ST_TIMEOUT_TICKS};
+
 template <class F, class SH>
 int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, int I, int topk, float eps,
                 uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out, float* xs_out,
@@ -655,12 +680,69 @@ int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, in
   if (!layers || !x || !ll || !sync) return -1;
   const void* k = reinterpret_cast<const void*>(&k_decode_step<F, SH>);
   if (!step_grid_ok(k)) return -1;
+  uint32_t* err = err_word();
+  if (err_pending() == DR_ERR_STEP_TIMEOUT) return DR_ERR_STEP_TIMEOUT;  // until dr_last_error clears it
   hipLaunchKernelGGL((k_decode_step<F, SH>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
-                     idx_out, wts_out, sgate_out, xs_out);
+                     idx_out, wts_out, sgate_out, xs_out, err, g_wait_ticks.load(std::memory_order_relaxed));
   return 0;
 }
 
+constexpr int ST_SCRATCH_WORDS = LL_WORDS + 2;  // ll, then sync[4] as two 64-bit words
+
 }  // namespace
+
+// ---- The entry point that allocates nothing (for callers that cannot allocate: code under
+// graph capture, serving loops, harnesses that forbid hipMalloc).  Its exchange buffer and sync
+// words are a file-scope device array, one copy per GPU, held until the process ends
+// (ST_SCRATCH_WORDS x 8 = 55,376 bytes).  Host code never passes the array's name: its address
+// on each device comes from hipGetSymbolAddress, looked up once per device with that device
+// current.  Calls that overlap on one GPU share the array and race; stream-order them.
+static __device__ __align__(256) uint64_t scratch[ST_SCRATCH_WORDS];
+
+namespace {
+
+__global__ void __launch_bounds__(256) k_zero_scratch(uint64_t* __restrict__ p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
+uint64_t* scratch_ptr() {
+  static std::atomic<uint64_t*> ptrs[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  uint64_t* p = ptrs[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    p = static_cast<uint64_t*>(q);
+    ptrs[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+}  // namespace
+
+API int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I,
+                                         int topk, float eps, int* idx_out, float* wts_out, float* sgate_out,
+                                         float* xs_out, dr_stream_t st) {
+  if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || n_layers < 1 || n_layers > ST_MAXL ||
+      !layers || !x)
+    return -1;
+  uint64_t* p = scratch_ptr();
+  if (!p) return (int)hipErrorInvalidSymbol;
+  // every call starts from cleared slots and sync words (a fill kernel: graph-capturable)
+  hipLaunchKernelGGL(k_zero_scratch, dim3(28), dim3(256), 0, (hipStream_t)st, p, ST_SCRATCH_WORDS);
+  return launch_step<StepQ4<ScaleBF16>, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, p,
+                                                   reinterpret_cast<uint32_t*>(p + LL_WORDS), idx_out, wts_out,
+                                                   sgate_out, xs_out, (hipStream_t)st);
+}
+
+API int dr_step_set_wait_limit(uint32_t us) {
+  g_wait_ticks.store(us ? (uint64_t)us * 100u : ST_TIMEOUT_TICKS, std::memory_order_relaxed);
+  return 0;
+}
 
 API int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, int E, int H, int I, int topk,
                            float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,

@@ -33,6 +33,12 @@
 extern "C" {
 #endif
 
+/* Library error codes (beside -1 and the raw HIP codes): a kernel whose bounded wait gave up
+ * sets a process-wide error word; dr_stream_sync reports it after the wait, the fused-step
+ * launchers refuse to start while it is set, and dr_last_error returns and clears it. */
+#define DR_ERR_STEP_TIMEOUT 9001 /* fused step: workgroups not co-resident within the wait limit */
+#define DR_ERR_PREFILL_WAIT 9002 /* prefill grouped GEMM: an LDS hand-off between waves timed out */
+
 typedef void* dr_stream_t;     /* hipStream_t */
 typedef void* dr_graph_exec_t; /* hipGraphExec_t */
 typedef uint16_t dr_bf16;      /* raw bf16 bits */
@@ -43,7 +49,7 @@ typedef uint16_t dr_half;      /* raw IEEE binary16 bits */
 /* ===================================================================================== */
 
 const char* dr_error_string(int e);                               /* src/ffi.rs:13 */
-int dr_last_error(void);                                          /* src/ffi.rs:14 */
+int dr_last_error(void);                                          /* src/ffi.rs:14 (+ library errors, cleared) */
 int dr_malloc(void** p, size_t n);                                /* src/ffi.rs:15 */
 int dr_free(void* p);                                             /* src/ffi.rs:16 */
 int dr_host_alloc(void** p, size_t n);                            /* src/ffi.rs:17 */
@@ -55,7 +61,7 @@ int dr_d2d(void* d, const void* s, size_t n, dr_stream_t st);     /* src/ffi.rs:
  * graph capture. */
 int dr_memset(void* d, int v, size_t n, dr_stream_t st);
 int dr_stream_create(dr_stream_t* s);                             /* src/ffi.rs:23, non-blocking */
-int dr_stream_sync(dr_stream_t s);                                /* src/ffi.rs:24 */
+int dr_stream_sync(dr_stream_t s);                                /* src/ffi.rs:24 (+ pending library error) */
 int dr_device_sync(void);                                         /* kernels/drama.cu:2012 */
 int dr_mem_info(size_t* free_b, size_t* total_b);                 /* src/ffi.rs:25 */
 int dr_graph_begin(dr_stream_t s);                                /* src/ffi.rs:26, thread-local capture */
@@ -133,7 +139,9 @@ int dr_moe_count(const int* idx, int n, int* counts, dr_stream_t st);
  * slot_of[i] = slot, xp[slot] = x[i / topk].  The within-expert order is stable in the pair
  * index (the reference's order comes from atomics and is unspecified; this is one of the
  * orders it can produce).  fill must be zero on entry and ends equal to the per-expert
- * counts, as in the reference.  Unsupported: rows * topk > 8192, h % 8 != 0 -> -1. */
+ * counts, as in the reference; only the entries of experts that occur in idx are read or
+ * written, so offsets/fill may hold just the model's E entries.  Pairs are grouped 8192 at a
+ * time in stream order (any rows * topk up to 2^30).  Unsupported: h % 8 != 0 -> -1. */
 int dr_moe_permute(const int* idx, int rows, int topk, const int* offsets, int* fill, int* slot_of,
                    const dr_bf16* x, dr_bf16* xp, int h, dr_stream_t st);
 
@@ -246,8 +254,11 @@ typedef struct dr_decode_layer {
  *   x         f32 [h], read at launch and overwritten with the last layer's output;
  *   ll        u64 [DR_STEP_LL_WORDS] exchange buffer, sync u32 [4]: both zeroed once by the
  *             caller before the first call and then left alone (a call advances sync[0]);
- *             sync[1] != 0 reports that a call timed out waiting for its workgroups (every
- *             later call then returns at once until the caller zeroes sync and ll again);
+ *             sync[1] != 0 reports that a call timed out waiting for its workgroups: that call
+ *             leaves x all NaN (blocks that gave up poison it) and raises DR_ERR_STEP_TIMEOUT,
+ *             which dr_stream_sync reports and dr_last_error returns and clears; until then the
+ *             step launchers return DR_ERR_STEP_TIMEOUT, and calls made before the caller zeroes
+ *             sync and ll again give up at once (NaN x, the error raised again);
  *   idx_out i32 [n_layers*8], wts_out f32 [n_layers*8], sgate_out f32 [n_layers],
  *   xs_out f32 [n_layers*h]: optional (NULL) per-layer routing and layer outputs.
  * Needs 256 co-resident workgroups of 512 threads (one MI355X); returns -1 otherwise.  Calls
@@ -258,6 +269,12 @@ int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, in
 int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                              int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                              float* sgate_out, float* xs_out, dr_stream_t st);
+/* Wait limit of the fused step's exchanges in microseconds (0 restores the default, 200000).
+ * A call whose workgroups are not all resident within the limit (another kernel holding CUs)
+ * gives up: x becomes NaN, sync[1] is set and DR_ERR_STEP_TIMEOUT is raised.  For tests that
+ * force that path from the host. */
+int dr_step_set_wait_limit(uint32_t us);
+
 /* The same step with block-FP8 routed experts: per layer gu_q/d_q are the e4m3 weights and
  * gu_s/d_s their 128 x 128 block scales of dr_moe_decode_fp8 (f32 scale_inv, int8 shared
  * scales f16 per 128) or of dr_moe_decode_fp8_bf16s (bf16 block scales, bf16 per-channel
@@ -270,6 +287,20 @@ int dr_moe_decode_step_fp8(const dr_decode_layer* layers, int n_layers, float* x
 int dr_moe_decode_step_fp8_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                                  int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                                  float* sgate_out, float* xs_out, dr_stream_t st);
+
+/* ===================================================================================== */
+/* Entry point that allocates nothing -- no counterpart in the reference.                 */
+/* ===================================================================================== */
+
+/* dr_moe_decode_step_bf16s without the caller's ll/sync buffers, for callers that cannot
+ * allocate (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The exchange buffer and sync words are a file-scope device array of 55,376 bytes, one per
+ * GPU, held until the process ends; each call clears it first (a fill kernel on st) and calls
+ * no allocator.  Calls that overlap on one GPU share the array and race: stream-order them.
+ * Same shapes and limits as dr_moe_decode_step_bf16s (n_layers <= 1365, else -1). */
+int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
+                                     int topk, float eps, int* idx_out, float* wts_out, float* sgate_out,
+                                     float* xs_out, dr_stream_t st);
 
 #ifdef __cplusplus
 }

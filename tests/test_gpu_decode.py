@@ -97,8 +97,10 @@ def test_decode_full_layer_e256_alias_and_bf16_output():
     assert np.abs(host(yb).view(np.uint16).astype(np.int32) - yb_ref).max() <= 1
 
 
-def test_router_then_decode_chain_40_layers_small():
-    """GPU router feeds GPU decode; indices are compared exactly at every layer."""
+def test_router_then_decode_chain_six_layers():
+    """Six layers of 32 experts: the GPU router feeds the GPU decode, each layer's input being
+    the previous GPU output; indices are compared exactly at every layer (the 40-layer,
+    256-expert configuration is tests/test_gpu_configs.py)."""
     import torch
 
     E, nl = 32, 6

@@ -102,6 +102,36 @@ def test_count_and_permute_reference_abi(rows):
     np.testing.assert_array_equal(xph[rs], x[np.arange(rows * topk) // topk])
 
 
+@pytest.mark.parametrize("rows,E", [(5, 8), (37, 24), (1100, 64)])
+def test_permute_touches_only_routed_experts(rows, E):
+    """offsets/fill sized for E < 256 experts with guard words behind them: the permute must
+    leave the guards alone (it reads and writes only experts that occur), and 1100 rows x 8
+    (8800 pairs, beyond one 8192-pair segment) must still give the stable slots."""
+    import torch
+
+    rng = np.random.default_rng(40 + rows)
+    topk = 8
+    idx = rng.integers(0, E, rows * topk).astype(np.int32)
+    if E > 8:
+        idx[idx == 3] = 4  # one expert that never occurs
+    x = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    rc, ro, rs = O.moe_group(idx, E)
+    guard = np.int32(-0x3C3C3C3D)
+    off_g = np.concatenate([ro, np.full(256, guard, np.int32)])
+    offsets, fill = dev(off_g), dev(np.concatenate([np.zeros(E, np.int32), np.full(256, guard, np.int32)]))
+    didx, slot_of, dx = dev(idx), t_i32(rows * topk), dev(x)
+    xp = torch.zeros(rows * topk * H, dtype=torch.int16, device="cuda")
+    D.lib().dr_moe_permute(D.ptr(didx), rows, topk, D.ptr(offsets), D.ptr(fill), D.ptr(slot_of), D.ptr(dx), D.ptr(xp),
+                           H, D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(slot_of), rs)
+    f = host(fill)
+    np.testing.assert_array_equal(f[:E], rc)
+    assert (f[E:] == guard).all() and (host(offsets)[E:] == guard).all(), "guard words after E entries changed"
+    xph = host(xp).view(np.uint16).reshape(rows * topk, H)
+    np.testing.assert_array_equal(xph[rs], x[np.arange(rows * topk) // topk])
+
+
 def grouped_inputs(seed, E, rows, topk, skew=False):
     rng = np.random.default_rng(seed)
     n = rows * topk
@@ -279,3 +309,80 @@ def test_prefill_layer_chain(fmt):
     print(f"act flips routed {int((af != rf).sum())}, shared {int((saf != srf).sum())}; "
           f"max |err| {np.abs(got - ref).max():.2e}")
     assert not bad.any(), f"prefill layer output: {int(bad.sum())} outside tolerance + flip propagation"
+
+
+def test_reference_elementwise_entry_points():
+    """dr_dequant_q8 and dr_f32_to_bf16 bit for bit (one fp32 product / one RNE rounding,
+    kernels/drama.cu:1114-1164), dr_swiglu_rows within one bf16 rounding flip."""
+    import torch
+
+    rng = np.random.default_rng(90)
+    L, sp = D.lib(), D.stream_ptr()
+    q = rng.integers(-127, 128, (96, 512), dtype=np.int8)
+    s = synth.f32_to_f16((np.abs(rng.normal(0, 0.02, (96, 4))) + 1e-4).astype(np.float32))
+    out = torch.zeros(96 * 512, dtype=torch.int16, device="cuda")
+    L.dr_dequant_q8(D.ptr(dev(q)), D.ptr(dev(s)), D.ptr(out), 96, 512, sp)
+    x = rng.normal(0, 3, 5000).astype(np.float32)
+    x[:6] = [np.inf, -np.inf, np.nan, 0.0, -0.0, 3.4e38]
+    xb = torch.zeros(5000, dtype=torch.int16, device="cuda")
+    L.dr_f32_to_bf16(D.ptr(dev(x)), D.ptr(xb), 5000, sp)
+    rows, ii = 7, 512
+    hh = rng.normal(0, 2, (rows, 2 * ii)).astype(np.float32)
+    y = torch.zeros(rows * ii, dtype=torch.int16, device="cuda")
+    L.dr_swiglu_rows(D.ptr(dev(hh)), D.ptr(y), rows, ii, sp)
+    torch.cuda.synchronize()
+    sf = O.f16_to_f32(s)
+    want = synth.f32_to_bf16(q.astype(np.float32) * np.repeat(sf, 128, axis=1))
+    np.testing.assert_array_equal(host(out).view(np.uint16).reshape(96, 512), want)
+    got = host(xb).view(np.uint16)
+    np.testing.assert_array_equal(got[3:], synth.f32_to_bf16(x[3:]))
+    assert got[0] == 0x7F80 and got[1] == 0xFF80 and (got[2] & 0x7F80) == 0x7F80 and (got[2] & 0x7F)
+    g, u = hh[:, :ii].astype(np.float64), hh[:, ii:].astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    check_act(host(y).view(np.uint16).reshape(rows, ii), synth.f32_to_bf16(ref.astype(np.float32)), "swiglu rows")
+
+
+def test_reference_shared_expert_sequence_300_rows():
+    """The unchanged engine's shared-expert prefill (src/engine.rs:351-355,560-562):
+    dr_dequant_q8 -> dr_gemm (300 x 1024 x 2048) -> dr_swiglu_rows -> dr_dequant_q8 -> dr_gemm
+    (300 x 2048 x 512).  Each GEMM equals the oracle's canonical-order GEMM bit for bit on the
+    GPU's own operands; the output is within the tolerance (plus act rounding flips) of the
+    float64 computation on the bf16-dequantised weights the reference multiplies."""
+    import torch
+
+    rows = 300
+    Lh = synth.make_layer(95, E=8, fmt="ref")
+    rng = np.random.default_rng(96)
+    hn = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    L, sp, P = D.lib(), D.stream_ptr(), D.ptr
+    h = np.zeros(1, np.uint64)
+    L.dr_cublas_create(h.ctypes.data, sp)
+    wbuf = torch.zeros(2 * I * H, dtype=torch.int16, device="cuda")
+    shh = torch.zeros(rows * 2 * I, device="cuda")
+    act = torch.zeros(rows * I, dtype=torch.int16, device="cuda")
+    out = torch.zeros(rows * H, device="cuda")
+    dhn = dev(hn)
+    L.dr_dequant_q8(P(dev(Lh["sgu_q"])), P(dev(Lh["sgu_s"])), P(wbuf), 2 * I, H, sp)
+    torch.cuda.synchronize()
+    wgu = host(wbuf).view(np.uint16).reshape(2 * I, H).copy()
+    L.dr_gemm(int(h[0]), P(dhn), P(wbuf), P(shh), rows, 2 * I, H, 0.0)
+    L.dr_swiglu_rows(P(shh), P(act), rows, I, sp)
+    torch.cuda.synchronize()
+    g_shh = host(shh).reshape(rows, 2 * I)
+    g_act = host(act).view(np.uint16).reshape(rows, I)
+    L.dr_dequant_q8(P(dev(Lh["sd_q"])), P(dev(Lh["sd_s"])), P(wbuf), H, I, sp)
+    torch.cuda.synchronize()
+    wd = host(wbuf).view(np.uint16)[:H * I].reshape(H, I).copy()
+    L.dr_gemm(int(h[0]), P(act), P(wbuf), P(out), rows, H, I, 0.0)
+    torch.cuda.synchronize()
+    g_out = host(out).reshape(rows, H)
+    # each GEMM: canonical order, bit for bit
+    np.testing.assert_array_equal(g_shh.view(np.uint32), O.router_logits_rows(hn, wgu, rows, 2 * I, H).view(np.uint32))
+    np.testing.assert_array_equal(g_out.view(np.uint32), O.router_logits_rows(g_act, wd, rows, H, I).view(np.uint32))
+    # end to end against float64 on the reference's bf16 weights
+    wguf = synth.bf16_to_f32(wgu).astype(np.float64)
+    wdf = synth.bf16_to_f32(wd).astype(np.float64)
+    hh = synth.bf16_to_f32(hn).astype(np.float64) @ wguf.T
+    ref_act = hh[:, :I] / (1 + np.exp(-hh[:, :I])) * hh[:, I:]
+    af, rf = check_act(g_act, synth.f32_to_bf16(ref_act.astype(np.float32)), "shared act (reference sequence)")
+    assert_close_with_flips(g_out, rf @ wdf.T, wdf, af, rf, "shared out (reference sequence)")

@@ -182,3 +182,86 @@ def test_step_graph_replays_match_eager():
         assert int(host(st.sync)[1]) == 0
     finally:
         L.dr_graph_destroy(g)
+
+
+def _clear_library_error():
+    L = D.lib()
+    L.raw("dr_last_error")()
+
+
+def test_step_gives_up_loudly_when_a_previous_call_timed_out():
+    """sync[1] set (what a timed-out call leaves behind) and not reset: the call must poison x
+    with NaN and raise DR_ERR_STEP_TIMEOUT; dr_stream_sync reports it, the launchers refuse to
+    start until dr_last_error has returned and cleared it, and after the caller zeroes sync and
+    ll the step is oracle-exact again."""
+    import torch
+
+    L = D.lib()
+    st = Stack([81, 82], 64, "cfg")
+    x0 = np.random.default_rng(12).normal(0, 1, H).astype(np.float32)
+    _clear_library_error()
+    try:
+        st.sync[1] = 1
+        xd = dev(x0)
+        args = [D.ptr(st.table), 2, D.ptr(xd), 64, H, I, TOPK, 1e-6, D.ptr(st.ll), D.ptr(st.sync), None, None, None,
+                None, D.stream_ptr()]
+        assert L.raw("dr_moe_decode_step_bf16s")(*args) == 0
+        assert L.raw("dr_stream_sync")(D.stream_ptr()) == 9001
+        assert np.isnan(host(xd)).all(), "a call that gave up must leave x all NaN"
+        assert L.raw("dr_moe_decode_step_bf16s")(*args) == 9001, "launcher must refuse while the error is pending"
+        assert L.raw("dr_last_error")() == 9001
+        assert L.raw("dr_last_error")() == 0, "dr_last_error clears the library error"
+        st.sync.zero_()
+        st.ll.zero_()
+        torch.cuda.synchronize()
+        xd = dev(x0)
+        r = st.run(xd)
+        assert L.raw("dr_stream_sync")(D.stream_ptr()) == 0
+        check_stack(st, x0, *r, host(xd))
+    finally:
+        _clear_library_error()
+
+
+def test_step_beside_a_busy_stream_is_correct_or_reports():
+    """Matrix products queued on a second stream hold CUs while the step launches, so its 256
+    workgroups may not all be resident at once.  With a 2 ms wait limit the step must either
+    give the oracle's bits or report DR_ERR_STEP_TIMEOUT with a NaN x; every kernel exits by
+    itself (the step's waits are bounded)."""
+    import torch
+
+    L = D.lib()
+    st = Stack([83, 84], 64, "cfg")
+    x0 = np.random.default_rng(13).normal(0, 1, H).astype(np.float32)
+    a = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
+    xd = dev(x0)
+    torch.cuda.synchronize()
+    _clear_library_error()
+    side = torch.cuda.Stream()
+    try:
+        L.dr_step_set_wait_limit(2000)
+        with torch.cuda.stream(side):
+            for _ in range(40):
+                a = (a @ a) * 1e-3
+        idx = torch.full((2 * TOPK,), -1, dtype=torch.int32, device="cuda")
+        wts = torch.zeros(2 * TOPK, device="cuda")
+        sg = torch.zeros(2, device="cuda")
+        xs = torch.zeros(2 * H, device="cuda")
+        main = torch.cuda.current_stream()
+        rc = L.raw("dr_moe_decode_step_bf16s")(D.ptr(st.table), 2, D.ptr(xd), 64, H, I, TOPK, 1e-6, D.ptr(st.ll),
+                                               D.ptr(st.sync), D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(xs),
+                                               main.cuda_stream)
+        assert rc == 0
+        code = L.raw("dr_stream_sync")(main.cuda_stream)
+        side.synchronize()
+        if code == 0:
+            print("step ran beside the busy stream and completed", flush=True)
+            check_stack(st, x0, host(idx).reshape(2, TOPK), host(wts).reshape(2, TOPK), host(sg),
+                        host(xs).reshape(2, H), host(xd))
+        else:
+            print("step gave up beside the busy stream (reported)", flush=True)
+            assert code == 9001
+            assert int(host(st.sync)[1]) == 1 and np.isnan(host(xd)).any()
+    finally:
+        L.dr_step_set_wait_limit(0)
+        torch.cuda.synchronize()
+        _clear_library_error()

@@ -125,6 +125,17 @@ class MoeStack:
         self.ll = torch.zeros(LL_WORDS, dtype=torch.int64, device=device)
         self.sync = torch.zeros(4, dtype=torch.int32, device=device)
         self.lib = dramamoe.lib()
+        self._gemm = {}  # stream handle -> GEMM handle (one per stream for the stack's lifetime)
+
+    def _gemm_handle(self, st) -> int:
+        import ctypes
+
+        key = int(st or 0)
+        if key not in self._gemm:
+            h = ctypes.c_void_p()
+            self.lib.dr_cublas_create(ctypes.byref(h), st)
+            self._gemm[key] = h.value
+        return self._gemm[key]
 
     def step(self, x, stream=None, idx_out=None, wts_out=None, sgate_out=None, xs_out=None) -> None:
         """x (f32 [H], device) through every loaded layer in one fused launch, in place."""
@@ -142,8 +153,6 @@ class MoeStack:
         8192 (row, expert) pairs per call): router GEMM, top-k, device-side grouping, gather,
         grouped expert GEMMs and the weighted combine, with the shared expert on a second stream
         beside them; no host round trip."""
-        import ctypes
-
         import torch
 
         P = dramamoe.ptr
@@ -152,16 +161,20 @@ class MoeStack:
         rows = x.shape[0]
         H, E, I, k = self.H, self.E, self.I, self.topk
         if chunk * k > 8192:
-            raise ValueError("chunk * topk must be <= 8192")
+            raise ValueError("chunk * topk must be <= 8192 (the pairs dr_moe_group sorts in one call)")
         c = min(chunk, rows)
         dev = x.device
-        z = lambda n, dt=torch.float32: torch.empty(n, dtype=dt, device=dev)
-        logits, idx, wts, sg = z(c * (E + 1)), z(c * k, torch.int32), z(c * k), z(c)
-        sact, sh = z(c * I, torch.int16), z(c * H)
-        counts, offsets, slot_of = z(E, torch.int32), z(E, torch.int32), z(c * k, torch.int32)
-        xp, act, yp = z(c * k * H, torch.int16), z(c * k * I, torch.int16), z(c * k * H)
-        h = ctypes.c_void_p()
-        lib.dr_cublas_create(ctypes.byref(h), st)
+        # temporaries come from the caching allocator of the stream the kernels run on, so they
+        # are not handed out again while this call's kernels are pending on it; the side stream
+        # waits for `main` before it touches them and `main` waits for it before the combine
+        main = torch.cuda.ExternalStream(st) if int(st) != 0 else torch.cuda.current_stream(dev)
+        with torch.cuda.stream(main):
+            z = lambda n, dt=torch.float32: torch.empty(n, dtype=dt, device=dev)
+            logits, idx, wts, sg = z(c * (E + 1)), z(c * k, torch.int32), z(c * k), z(c)
+            sact, sh = z(c * I, torch.int16), z(c * H)
+            counts, offsets, slot_of = z(E, torch.int32), z(E, torch.int32), z(c * k, torch.int32)
+            xp, act, yp = z(c * k * H, torch.int16), z(c * k * I, torch.int16), z(c * k * H)
+        gh = self._gemm_handle(st)
         # the shared expert needs only hn, so it runs on a second stream beside the routing,
         # grouping and gather and joins before the combine.  Only from a created stream: events
         # recorded through a wrapper of the null stream (handle 0) did not order the kernels
@@ -169,7 +182,6 @@ class MoeStack:
         # combine), so on the null stream everything stays in order on it.
         overlap = int(st) != 0 and c >= 64  # for a few rows the events cost more than they save
         if overlap:
-            main = torch.cuda.ExternalStream(st)
             side = torch.cuda.Stream(device=dev)
             fork, join = torch.cuda.Event(), torch.cuda.Event()
         for r0 in range(0, rows, c):
@@ -182,7 +194,7 @@ class MoeStack:
                                       P(sh), H, I, side.cuda_stream if overlap else st)
             if overlap:
                 join.record(side)
-            lib.dr_gemm(h.value, P(hr), P(L["router"]), P(logits), n, E + 1, H, 0.0)
+            lib.dr_gemm(gh, P(hr), P(L["router"]), P(logits), n, E + 1, H, 0.0)
             lib.dr_moe_topk(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), st)
             lib.dr_moe_group(P(idx), n * k, E, P(counts), P(offsets), P(slot_of), st)
             lib.dr_moe_gather_rows(P(slot_of), n, k, P(hr), P(xp), H, st)

@@ -321,15 +321,18 @@ def test_reference_elementwise_entry_points():
     q = rng.integers(-127, 128, (96, 512), dtype=np.int8)
     s = synth.f32_to_f16((np.abs(rng.normal(0, 0.02, (96, 4))) + 1e-4).astype(np.float32))
     out = torch.zeros(96 * 512, dtype=torch.int16, device="cuda")
-    L.dr_dequant_q8(D.ptr(dev(q)), D.ptr(dev(s)), D.ptr(out), 96, 512, sp)
+    dq, ds = dev(q), dev(s)  # kept alive until the kernels have run
+    L.dr_dequant_q8(D.ptr(dq), D.ptr(ds), D.ptr(out), 96, 512, sp)
     x = rng.normal(0, 3, 5000).astype(np.float32)
     x[:6] = [np.inf, -np.inf, np.nan, 0.0, -0.0, 3.4e38]
     xb = torch.zeros(5000, dtype=torch.int16, device="cuda")
-    L.dr_f32_to_bf16(D.ptr(dev(x)), D.ptr(xb), 5000, sp)
+    dxx = dev(x)
+    L.dr_f32_to_bf16(D.ptr(dxx), D.ptr(xb), 5000, sp)
     rows, ii = 7, 512
     hh = rng.normal(0, 2, (rows, 2 * ii)).astype(np.float32)
     y = torch.zeros(rows * ii, dtype=torch.int16, device="cuda")
-    L.dr_swiglu_rows(D.ptr(dev(hh)), D.ptr(y), rows, ii, sp)
+    dhh = dev(hh)
+    L.dr_swiglu_rows(D.ptr(dhh), D.ptr(y), rows, ii, sp)
     torch.cuda.synchronize()
     sf = O.f16_to_f32(s)
     want = synth.f32_to_bf16(q.astype(np.float32) * np.repeat(sf, 128, axis=1))
@@ -362,7 +365,8 @@ def test_reference_shared_expert_sequence_300_rows():
     act = torch.zeros(rows * I, dtype=torch.int16, device="cuda")
     out = torch.zeros(rows * H, device="cuda")
     dhn = dev(hn)
-    L.dr_dequant_q8(P(dev(Lh["sgu_q"])), P(dev(Lh["sgu_s"])), P(wbuf), 2 * I, H, sp)
+    w = {k: dev(Lh[k]) for k in ("sgu_q", "sgu_s", "sd_q", "sd_s")}
+    L.dr_dequant_q8(P(w["sgu_q"]), P(w["sgu_s"]), P(wbuf), 2 * I, H, sp)
     torch.cuda.synchronize()
     wgu = host(wbuf).view(np.uint16).reshape(2 * I, H).copy()
     L.dr_gemm(int(h[0]), P(dhn), P(wbuf), P(shh), rows, 2 * I, H, 0.0)
@@ -370,7 +374,7 @@ def test_reference_shared_expert_sequence_300_rows():
     torch.cuda.synchronize()
     g_shh = host(shh).reshape(rows, 2 * I)
     g_act = host(act).view(np.uint16).reshape(rows, I)
-    L.dr_dequant_q8(P(dev(Lh["sd_q"])), P(dev(Lh["sd_s"])), P(wbuf), H, I, sp)
+    L.dr_dequant_q8(P(w["sd_q"]), P(w["sd_s"]), P(wbuf), H, I, sp)
     torch.cuda.synchronize()
     wd = host(wbuf).view(np.uint16)[:H * I].reshape(H, I).copy()
     L.dr_gemm(int(h[0]), P(act), P(wbuf), P(out), rows, H, I, 0.0)

@@ -125,7 +125,8 @@ def test_moe_topk_special_values():
     idx = torch.empty(rows * 8, dtype=torch.int32, device="cuda")
     wts = torch.empty(rows * 8, dtype=torch.float32, device="cuda")
     sg = torch.empty(rows, dtype=torch.float32, device="cuda")
-    D.lib().dr_moe_topk(D.ptr(dev(lg)), rows, E, 8, stride, D.ptr(idx), D.ptr(wts), D.ptr(sg), D.stream_ptr())
+    dlg = dev(lg)  # kept alive until the kernel has run
+    D.lib().dr_moe_topk(D.ptr(dlg), rows, E, 8, stride, D.ptr(idx), D.ptr(wts), D.ptr(sg), D.stream_ptr())
     torch.cuda.synchronize()
     hi, hw, hs = host(idx), host(wts), host(sg)
     np.testing.assert_array_equal(hi, ri)

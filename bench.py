@@ -193,7 +193,7 @@ def main():
         sg = torch.zeros(1, device="cuda")
         counter = torch.zeros(4, dtype=torch.int32, device="cuda")
         act = torch.zeros((TOPK + 1) * I, device="cuda")
-        ll = torch.zeros(6920, dtype=torch.int64, device="cuda")
+        ll = torch.zeros(D.STEP_LL_WORDS, dtype=torch.int64, device="cuda")
         sync = torch.zeros(4, dtype=torch.int32, device="cuda")
         keys = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")
         table = torch.tensor([[Lr[k].data_ptr() for k in keys] for Lr in layers], dtype=torch.int64, device="cuda")

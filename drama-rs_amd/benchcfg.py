@@ -268,7 +268,7 @@ def config5_fp8(lib, st, iters=100, copies=4):
     routers = [bf16_bits(torch.randn(E + 1, H, generator=gr, device="cuda") * 0.02) for _ in range(nl)]
     table = torch.tensor([[(routers[l] if k == "router" else Ls[l % copies][k]).data_ptr() for k in keys]
                           for l in range(nl)], dtype=torch.int64, device="cuda")
-    ll, sync = z(6920, torch.int64), z(4, torch.int32)
+    ll, sync = z(D.STEP_LL_WORDS, torch.int64), z(4, torch.int32)
 
     def fused(i):
         lib.dr_moe_decode_step_fp8_bf16s(P(table), nl, P(x), E, H, I, TOPK, 1e-6, P(ll), P(sync), None, None, None,

@@ -26,7 +26,7 @@ import dramamoe
 
 FORMAT = "drama-rs-v1"
 Q4_GROUP, Q8_GROUP = 64, 128
-LL_WORDS = 6920  # DR_STEP_LL_WORDS
+LL_WORDS = dramamoe.STEP_LL_WORDS
 
 
 class CheckpointError(ValueError):

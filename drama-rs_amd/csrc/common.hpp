@@ -27,6 +27,31 @@ DEV void raise_err(uint32_t* err, uint32_t code) {
   if (err) __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Loads from global memory, explicitly in the global address space: a pointer read out of a
+// table (rather than passed as a kernel argument) is otherwise generic, and generic (flat)
+// loads count against both the vector-memory and the LDS counters, so every wait for an LDS
+// value would also wait for all weight loads in flight.
+typedef uint32_t gu32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gu32x2 __attribute__((ext_vector_type(2)));
+template <class T>
+DEV T gld(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+DEV uint4 ld16(const void* p) {
+  const gu32x4 v = gld<gu32x4>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+DEV uint2 ld8(const void* p) {
+  const gu32x2 v = gld<gu32x2>(p);
+  return make_uint2(v.x, v.y);
+}
+DEV float4 ldf4(const void* p) {
+  const gu32x4 v = gld<gu32x4>(p);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+DEV uint32_t ld4(const void* p) { return gld<uint32_t>(p); }
+DEV uint32_t ld2(const void* p) { return gld<uint16_t>(p); }
+
 DEV float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
 DEV float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 DEV float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
@@ -127,8 +152,16 @@ DEV void lds_barrier() {
 // Block-FP8 helpers: one scale per 128 x 128 block, f32 (SF = 0, the reference's scale_inv)
 // or bf16 (SF = 1); e4m3 bytes convert to f32 exactly with v_cvt_pk_f32_fp8.
 template <int SF>
+DEV uint32_t blk_raw(const void* S, size_t i) {
+  return SF ? ld2(reinterpret_cast<const uint16_t*>(S) + i) : ld4(reinterpret_cast<const float*>(S) + i);
+}
+template <int SF>
+DEV float blk_cvt(uint32_t r) {
+  return SF ? bf16f(r) : __uint_as_float(r);
+}
+template <int SF>
 DEV float blk_scale(const void* S, size_t i) {
-  return SF ? bf16f(reinterpret_cast<const uint16_t*>(S)[i]) : reinterpret_cast<const float*>(S)[i];
+  return blk_cvt<SF>(blk_raw<SF>(S, i));
 }
 
 // sum_{i<16} e4m3(w bytes) * x[i]
@@ -162,12 +195,17 @@ struct ScaleBF16 {
 };
 
 // int8 scale of element k of row n for a K-wide int8 matrix.
+// raw() loads the scale's bits, cvt() converts them (so a load can be issued long before use).
 struct Q8G128F16 {  // reference layout: f16 scale per 128 inputs, s [N, K/128]
-  static DEV float scale(const uint16_t* s, size_t n, int k, int K) { return f16f(s[n * (K / 128) + (k >> 7)]); }
+  static DEV uint32_t raw(const uint16_t* s, size_t n, int k, int K) { return ld2(s + n * (K / 128) + (k >> 7)); }
+  static DEV float cvt(uint32_t r) { return f16f(r); }
+  static DEV float scale(const uint16_t* s, size_t n, int k, int K) { return cvt(raw(s, n, k, K)); }
   static constexpr bool per_row = false;
 };
 struct Q8RowBF16 {  // per-output-channel bf16 scale, s [N]
-  static DEV float scale(const uint16_t* s, size_t n, int, int) { return bf16f(s[n]); }
+  static DEV uint32_t raw(const uint16_t* s, size_t n, int, int) { return ld2(s + n); }
+  static DEV float cvt(uint32_t r) { return bf16f(r); }
+  static DEV float scale(const uint16_t* s, size_t n, int k, int K) { return cvt(raw(s, n, k, K)); }
   static constexpr bool per_row = true;
 };
 
@@ -198,9 +236,7 @@ DEV float dot4_u8b(uint32_t w, const float* x, float acc) {
   return acc;
 }
 
-// Plain 16-byte global load.
-DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
-DEV uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
+
 
 // Touch [pf, pf + bytes) so the data sits in the memory-side cache (MALL) for the next
 // kernel.  Each block takes an equal share; the loaded words are folded into a register

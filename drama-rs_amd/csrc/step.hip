@@ -41,7 +41,6 @@ constexpr int ST_H = 2048, ST_I = 512, ST_TOPK = 8, ST_MAXE = 256;
 constexpr int ST_NB = 256, ST_WPB = 8, ST_NT = ST_WPB * 64, ST_NP = 8;  // every wave polls a share
 constexpr uint32_t ST_TAG_STRIDE = 4096;
 constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
-constexpr int ST_TABL = 48;  // layer records staged in LDS (scalar loads on the critical path cost ~1 us)
 // When each wave polls an exchange for the first time, in 10 ns ticks of s_memrealtime after
 // a point every wave of the block passes together (so the waves that reach an exchange early,
 // like the non-router waves at the logits, do not poll before the data can be there): the
@@ -227,8 +226,8 @@ struct StepQ4 {
       const int j = rj + p;
       g.wg[p] = ld16(q + (size_t)j * (H / 2));
       g.wu[p] = ld16(q + (size_t)(I + j) * (H / 2));
-      g.sg[p] = sm[(size_t)j * (H / 64)];
-      g.su[p] = sm[(size_t)(I + j) * (H / 64)];
+      g.sg[p] = ld4(sm + (size_t)j * (H / 64));
+      g.su[p] = ld4(sm + (size_t)(I + j) * (H / 64));
     }
   }
   DEV static void gate_up(const GU& g, const float4* xq4, const float* s_xsum, int lane, float (&av)[2]) {
@@ -263,8 +262,8 @@ struct StepQ4 {
     const uint32_t* dsm = reinterpret_cast<const uint32_t*>(Ly.d_s);
     d.qa = ld16(Ly.d_q + (ea * H + n) * (I / 2) + cc * 16);
     d.qb = ld16(Ly.d_q + (eb * H + n) * (I / 2) + cc * 16);
-    d.sa = dsm[(ea * H + n) * (I / 64) + (cc >> 1)];
-    d.sb = dsm[(eb * H + n) * (I / 64) + (cc >> 1)];
+    d.sa = ld4(dsm + (ea * H + n) * (I / 64) + (cc >> 1));
+    d.sb = ld4(dsm + (eb * H + n) * (I / 64) + (cc >> 1));
   }
   DEV static float down(const DN& d, const float4* as4, const float* s_asum, float my_w, int lane) {
     const int ka = lane >> 4;
@@ -300,7 +299,7 @@ struct StepFP8 {
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];
-    float sg[2][2], su[2][2];
+    uint32_t sg[2][2], su[2][2];  // raw scale bits
   };
   DEV static void load_gu(const dr_decode_layer& Ly, size_t ek, int rj, int lane, GU& g) {
     constexpr int H = ST_H, I = ST_I;
@@ -311,10 +310,10 @@ struct StepFP8 {
       const int j = rj + p;
       g.g[p][0] = ld16(w + (size_t)j * H), g.g[p][1] = ld16(w + (size_t)j * H + 1024);
       g.u[p][0] = ld16(w + (size_t)(I + j) * H), g.u[p][1] = ld16(w + (size_t)(I + j) * H + 1024);
-      g.sg[p][0] = blk_scale<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128));
-      g.sg[p][1] = blk_scale<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128) + 8);
-      g.su[p][0] = blk_scale<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128));
-      g.su[p][1] = blk_scale<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128) + 8);
+      g.sg[p][0] = blk_raw<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128));
+      g.sg[p][1] = blk_raw<SF>(Ly.gu_s, sb + (size_t)(j >> 7) * (H / 128) + 8);
+      g.su[p][0] = blk_raw<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128));
+      g.su[p][1] = blk_raw<SF>(Ly.gu_s, sb + (size_t)((I + j) >> 7) * (H / 128) + 8);
     }
   }
   DEV static void gate_up(const GU& g, const float4* xq4, const float*, int lane, float (&av)[2]) {
@@ -327,14 +326,16 @@ struct StepFP8 {
     }
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const float gv = wave_sum(g.sg[p][0] * dot16_fp8(g.g[p][0], xa, 0.f) + g.sg[p][1] * dot16_fp8(g.g[p][1], xb, 0.f));
-      const float uv = wave_sum(g.su[p][0] * dot16_fp8(g.u[p][0], xa, 0.f) + g.su[p][1] * dot16_fp8(g.u[p][1], xb, 0.f));
+      const float gv = wave_sum(blk_cvt<SF>(g.sg[p][0]) * dot16_fp8(g.g[p][0], xa, 0.f) +
+                                blk_cvt<SF>(g.sg[p][1]) * dot16_fp8(g.g[p][1], xb, 0.f));
+      const float uv = wave_sum(blk_cvt<SF>(g.su[p][0]) * dot16_fp8(g.u[p][0], xa, 0.f) +
+                                blk_cvt<SF>(g.su[p][1]) * dot16_fp8(g.u[p][1], xb, 0.f));
       av[p] = silu(gv) * uv;
     }
   }
   struct DN {
     uint4 q[4];
-    float sc[4];
+    uint32_t sc[4];  // raw scale bits
   };
   DEV static void load_dn(const dr_decode_layer& Ly, int my_idx, int n, int lane, DN& d) {
     constexpr int H = ST_H, I = ST_I;
@@ -343,7 +344,7 @@ struct StepFP8 {
     for (int i = 0; i < 4; ++i) {
       const size_t e = (size_t)__shfl(my_idx, 2 * i + half);
       d.q[i] = ld16(Ly.d_q + (e * H + n) * I + cc * 16);
-      d.sc[i] = blk_scale<SF>(Ly.d_s, (e * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
+      d.sc[i] = blk_raw<SF>(Ly.d_s, (e * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
     }
   }
   DEV static float down(const DN& d, const float4* as4, const float*, float my_w, int lane) {
@@ -357,7 +358,7 @@ struct StepFP8 {
         const float4 v = as4[256 * i + t * 64 + lane];
         xa[4 * t] = v.x, xa[4 * t + 1] = v.y, xa[4 * t + 2] = v.z, xa[4 * t + 3] = v.w;
       }
-      acc += __shfl(my_w, 2 * i + half) * d.sc[i] * dot16_fp8(d.q[i], xa, 0.f);
+      acc += __shfl(my_w, 2 * i + half) * blk_cvt<SF>(d.sc[i]) * dot16_fp8(d.q[i], xa, 0.f);
     }
     return acc;
   }
@@ -373,7 +374,7 @@ struct RouterRow {
 };
 struct SharedPair {
   uint4 g0, g1, u0, u1;
-  float sg0, sg1, su0, su1;
+  uint32_t sg0, sg1, su0, su1;  // raw scale bits (SH::cvt at use)
 };
 
 template <class SH>
@@ -382,8 +383,8 @@ DEV void load_shared_pair(const dr_decode_layer& Ly, int j, int lane, SharedPair
   const int8_t* rg = Ly.sgu_q + (size_t)j * H + lane * 16;
   const int8_t* ru = Ly.sgu_q + (size_t)(I + j) * H + lane * 16;
   s.g0 = ld16(rg), s.g1 = ld16(rg + 1024), s.u0 = ld16(ru), s.u1 = ld16(ru + 1024);
-  s.sg0 = SH::scale(Ly.sgu_s, j, lane * 16, H), s.sg1 = SH::scale(Ly.sgu_s, j, 1024 + lane * 16, H);
-  s.su0 = SH::scale(Ly.sgu_s, I + j, lane * 16, H), s.su1 = SH::scale(Ly.sgu_s, I + j, 1024 + lane * 16, H);
+  s.sg0 = SH::raw(Ly.sgu_s, j, lane * 16, H), s.sg1 = SH::raw(Ly.sgu_s, j, 1024 + lane * 16, H);
+  s.su0 = SH::raw(Ly.sgu_s, I + j, lane * 16, H), s.su1 = SH::raw(Ly.sgu_s, I + j, 1024 + lane * 16, H);
 }
 
 template <class F, class SH>
@@ -404,7 +405,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ uint64_t s_cand[32];  // per-group top 8 (canon_cand64)
   __shared__ float s_mz[2];
   __shared__ int s_abort;
-  __shared__ dr_decode_layer s_tab[ST_TABL];  // the first ST_TABL layer records
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   // A block that gives up (a bounded wait expired, or an earlier call did and sync was not
   // reset) poisons the whole output with NaN and raises DR_ERR_STEP_TIMEOUT, so a failed call
@@ -436,30 +436,26 @@ __global__ void __launch_bounds__(ST_NT, 1)
   SharedPair sp;
   float4 nwv = make_float4(1.f, 1.f, 1.f, 1.f);
   if (tid == 0) s_abort = 0;
+  // layer records travel in scalar registers (read with scalar loads a layer ahead): staged
+  // in LDS or read through a generic pointer they would turn every weight load into a flat
+  // load, whose waits also drain the LDS counter
+  dr_decode_layer Ly = layers[0];
   {
-    const int nw32 = (L < ST_TABL ? L : ST_TABL) * (int)(sizeof(dr_decode_layer) / 4);
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(layers);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(s_tab);
-    for (int i = tid; i < nw32; i += ST_NT) dst[i] = src[i];
-  }
-  __syncthreads();
-  auto layer = [&](int i) { return i < ST_TABL ? s_tab[i] : layers[i]; };
-  {
-    const dr_decode_layer L0 = layer(0);
+    const dr_decode_layer& L0 = Ly;
     if (is_router) {
       const uint16_t* wr = L0.router + (size_t)rrow * H;
 #pragma unroll
       for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
     }
     if (is_shared) load_shared_pair<SH>(L0, sj, lane, sp);
-    if (L0.nw) nwv = reinterpret_cast<const float4*>(L0.nw)[tid];
+    if (L0.nw) nwv = ldf4(L0.nw + 4 * tid);
     nws[tid] = nwv;
     xr4[tid] = reinterpret_cast<const float4*>(x)[tid];
   }
   __syncthreads();
 
+  dr_decode_layer Ln = Ly;
   for (int l = 0; l < L; ++l) {
-    const dr_decode_layer Ly = layer(l);
     const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2;
     ST_MARK(0);
     const uint64_t t_layer = __builtin_amdgcn_s_memrealtime();
@@ -513,8 +509,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
           ga = dot4_u8b(gw0[d], xa + 4 * d, ga), gb = dot4_u8b(gw1[d], xb + 4 * d, gb);
           ua = dot4_u8b(uw0[d], xa + 4 * d, ua), ub = dot4_u8b(uw1[d], xb + 4 * d, ub);
         }
-        const float gv = wave_sum(sp.sg0 * (ga - 128.f * sa) + sp.sg1 * (gb - 128.f * sb));
-        const float uv = wave_sum(sp.su0 * (ua - 128.f * sa) + sp.su1 * (ub - 128.f * sb));
+        const float gv = wave_sum(SH::cvt(sp.sg0) * (ga - 128.f * sa) + SH::cvt(sp.sg1) * (gb - 128.f * sb));
+        const float uv = wave_sum(SH::cvt(sp.su0) * (ua - 128.f * sa) + SH::cvt(sp.su1) * (ub - 128.f * sb));
         if (lane == 0) ll_put(ll + LL_ACT + ST_TOPK * I / 2 + sj, silu(gv) * uv, tB);
       }
       ST_MARK(1);
@@ -576,7 +572,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       typename F::DN dn;
       F::load_dn(Ly, my_idx, n, lane, dn);
       const uint2 qs = ld8(Ly.sd_q + (size_t)n * I + lane * 8);
-      const float ssc = SH::scale(Ly.sd_s, n, lane * 8, I);
+      const uint32_t ssr = SH::raw(Ly.sd_s, n, lane * 8, I);
 
       // ---- activation exchange, collected by the poller
       ST_MARKW(14, 2);
@@ -599,15 +595,16 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
       // ---- next layer's known weights: issued after the activation poll (a wave's loads
       // return in order, so loads issued before a poll would delay it)
+      Ln = Ly;
       if (l + 1 < L) {
-        const dr_decode_layer Ln = layer(l + 1);
+        Ln = layers[l + 1];
         if (is_router) {
           const uint16_t* wr = Ln.router + (size_t)rrow * H;
 #pragma unroll
           for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
         }
         if (is_shared) load_shared_pair<SH>(Ln, sj, lane, sp);
-        nwv = Ln.nw ? reinterpret_cast<const float4*>(Ln.nw)[tid] : make_float4(1.f, 1.f, 1.f, 1.f);
+        nwv = Ln.nw ? ldf4(Ln.nw + 4 * tid) : make_float4(1.f, 1.f, 1.f, 1.f);
       }
 
       // ---- routing weights (s_mz is complete since the activation barrier)
@@ -629,7 +626,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       }
       float dc = dot4_u8b(qs.x, xc, 0.f);
       dc = dot4_u8b(qs.y, xc + 4, dc);
-      float acc = F::down(dn, as4, s_asum, my_w, lane) + sgv * ssc * (dc - 128.f * sumc);
+      float acc = F::down(dn, as4, s_asum, my_w, lane) + sgv * SH::cvt(ssr) * (dc - 128.f * sumc);
       acc = wave_sum(acc);
       if (lane == 0) {
         const float y = res + acc;
@@ -652,6 +649,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       give_up();
       return;
     }
+    Ly = Ln;
   }
   if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

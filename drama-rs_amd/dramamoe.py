@@ -59,6 +59,14 @@ def _ret_type(r: str):
     return _TYPES[r]
 
 
+def header_define(name: str, path: str = HEADER) -> int:
+    """Integer value of a #define in the header (e.g. DR_STEP_LL_WORDS)."""
+    m = re.search(r"#define\s+" + name + r"\s+(\d+)", open(path).read())
+    if not m:
+        raise KeyError(name)
+    return int(m.group(1))
+
+
 class DramaMoeError(RuntimeError):
     pass
 
@@ -103,6 +111,7 @@ class Lib:
 
 
 _lib: Lib | None = None
+STEP_LL_WORDS = header_define("DR_STEP_LL_WORDS")
 
 
 def build() -> None:

@@ -125,7 +125,7 @@ def test_cfg3_forty_layer_step_full_size():
     print("cfg3: generating 40 layers x 256 int4 experts on the device", flush=True)
     layers = [bench.make_layer_gpu(None, l) for l in range(nl)]
     table = torch.tensor([[Lr[k].data_ptr() for k in KEYS] for Lr in layers], dtype=torch.int64, device="cuda")
-    ll = torch.zeros(6920, dtype=torch.int64, device="cuda")
+    ll = torch.zeros(D.STEP_LL_WORDS, dtype=torch.int64, device="cuda")
     sync = torch.zeros(4, dtype=torch.int32, device="cuda")
     idx = torch.full((nl * TOPK,), -1, dtype=torch.int32, device="cuda")
     wts = torch.zeros(nl * TOPK, device="cuda")

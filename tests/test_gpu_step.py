@@ -15,7 +15,7 @@ from helpers import assert_close, bits, dev, host
 pytestmark = pytest.mark.gpu
 
 H, I, TOPK = 2048, 512, 8
-LL_WORDS = 6920
+LL_WORDS = D.STEP_LL_WORDS
 KEYS = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")
 
 

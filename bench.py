@@ -310,6 +310,21 @@ def main():
     lib.dr_graph_destroy(fexec)
     fused_ok = int(sync[1].item()) == 0
 
+    # ---- the same step with the routed activations exchanged as 24-bit floats (opt-in mode)
+    fused_a24_ms = float("nan")
+    if not args.profile:
+        lib.dr_step_set_act_exchange(24)
+        for _ in range(args.warmup):
+            fused_step()
+        torch.cuda.synchronize()
+        fe0.record(st)
+        for _ in range(args.steps):
+            fused_step()
+        fe1.record(st)
+        torch.cuda.synchronize()
+        fused_a24_ms = fe0.elapsed_time(fe1) / args.steps
+        lib.dr_step_set_act_exchange(32)
+
     # ---- per-layer kernel chain (router, gate_up, down per layer): eager and graph timing
     eager_ms = graph_ms = float("nan")
     if not args.profile:
@@ -355,7 +370,10 @@ def main():
             import numpy as np
             import oracle as O
 
-            threads = min(os.cpu_count() or 1, 16)
+            # every core this process may use: the affinity set, bounded by OMP_NUM_THREADS
+            # where the host sets it (one GPU's share of the GPU box's host is 16 cores)
+            avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+            threads = min(avail, int(os.environ.get("OMP_NUM_THREADS", avail)))
             O.lib().or_set_threads(threads)
             xs = x0
             n, t_cpu = 0, 0.0
@@ -376,6 +394,8 @@ def main():
                 n1 += 1
             O.lib().or_set_threads(threads)
             cpu = {"value": round(t_cpu / n * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+                   "cores_note": f"all {threads} cores available to this process (affinity {avail}, "
+                                 f"OMP_NUM_THREADS {os.environ.get('OMP_NUM_THREADS', 'unset')})",
                    "sample": f"{n} decode layers (router + 8 int4 experts + int8 shared, fp64 accumulation) of layer 0, "
                              f"{t_cpu:.1f} s",
                    "value_1thread": round(t1s / n1 * 1e6, 1),
@@ -397,13 +417,19 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights, fp32 accumulate",
+        "dtype": "int4 weights, fp32 accumulate, fp32 activations between workgroups",
         "data": "synthetic (seeded torch RNG on device, shapes of BASELINE config 3)",
         "config": {"workload": "cfg3: 40-layer int4 routed-expert decode step, batch 1, top-8 of 256, hidden 2048, "
                                "expert intermediate 512, int8 shared expert; one fused persistent launch per step "
                                "(dr_moe_decode_step_bf16s)",
                    "layers": nl, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I},
         "fused_graph_ms_per_step": round(fused_graph_ms, 4),
+        "fused_act24_us_per_layer": None if args.profile else round(fused_a24_ms * 1000.0 / nl, 3),
+        "fused_act24_note": "the same step with the routed activations exchanged as 24-bit floats "
+                            "(dr_step_set_act_exchange(24), relative error <= 2^-16)",
+        "engine_one_layer_us": (extra or {}).get("cfg2_one_layer", {}).get("fused_one_layer", {}).get("us"),
+        "engine_one_layer_note": "one MoE layer per launch (the engine interleaves attention between MoE "
+                                 "layers, so a drop-in caller launches the step with n_layers = 1)",
         "fused_graph_us_per_layer": round(fused_graph_ms * 1000.0 / nl, 3),
         "chain_eager_us_per_layer": None if args.profile else round(eager_ms * 1000.0 / nl, 3),
         "chain_graph_us_per_layer": None if args.profile else round(graph_ms * 1000.0 / nl, 3),

@@ -55,8 +55,9 @@ def _expect(prefix, name, t, dtype, shape):
     return t.contiguous() if isinstance(t, torch.Tensor) else t
 
 
-def read_layer(path: str, i: int, tc: dict) -> dict:
-    """Host tensors (torch, CPU) of layer i's MoE, checked against the config."""
+def read_layer(path: str, i: int, tc: dict, experts: bool = True) -> dict:
+    """Host tensors (torch, CPU) of layer i's MoE, checked against the config; experts=False
+    skips the int4 routed experts (when they come from an FP8 source)."""
     import torch
     from safetensors import safe_open
 
@@ -74,10 +75,11 @@ def read_layer(path: str, i: int, tc: dict) -> dict:
 
         out["nw"] = get("post_norm", torch.float32, (H,))
         out["router"] = get("moe.router", torch.bfloat16, (E + 1, H))
-        out["gu_q"] = get("moe.gate_up.q4", torch.uint8, (E, 2 * I, H // 2))
-        out["gu_s"] = get("moe.gate_up.sm", torch.float16, (E, 2 * I, H // Q4_GROUP, 2))
-        out["d_q"] = get("moe.down.q4", torch.uint8, (E, H, I // 2))
-        out["d_s"] = get("moe.down.sm", torch.float16, (E, H, I // Q4_GROUP, 2))
+        if experts:
+            out["gu_q"] = get("moe.gate_up.q4", torch.uint8, (E, 2 * I, H // 2))
+            out["gu_s"] = get("moe.gate_up.sm", torch.float16, (E, 2 * I, H // Q4_GROUP, 2))
+            out["d_q"] = get("moe.down.q4", torch.uint8, (E, H, I // 2))
+            out["d_s"] = get("moe.down.sm", torch.float16, (E, H, I // Q4_GROUP, 2))
         out["sgu_q"] = get("moe.shared_gate_up.q8", torch.int8, (2 * I, H))
         out["sgu_s"] = get("moe.shared_gate_up.s", torch.float16, (2 * I, H // Q8_GROUP))
         out["sd_q"] = get("moe.shared_down.q8", torch.int8, (H, I))
@@ -104,13 +106,85 @@ def write_meta(path: str, H: int, E: int, I: int, layers: int, topk: int = 8, ep
                   indent=1)
 
 
+FP8_BLOCK = 128
+
+
+class Fp8Source:
+    """Routed experts in their original block-FP8 form, read from the source checkpoint (the
+    reference's Fp8Source, src/model.rs:406-506): ``model.safetensors.index.json`` maps every
+    tensor to its shard; expert ex of layer li is
+
+        model.language_model.layers.{li}.mlp.experts.{ex}.{gate,up,down}_proj.weight
+            F8_E4M3 [I, H] (gate, up) / [H, I] (down)
+        ....weight_scale_inv   F32 [rows / 128, cols / 128]
+
+    ``layer`` assembles the layouts the FP8 kernels take (src/model.rs:99-100): gate_up w
+    [E, 2I, H] (gate rows, then up rows) with s [E, 2I/128, H/128], down w [E, H, I] with
+    s [E, H/128, I/128]; dtypes and shapes are checked with the reference's messages."""
+
+    def __init__(self, path: str):
+        fn = os.path.join(path, "model.safetensors.index.json")
+        try:
+            with open(fn) as f:
+                self.weight_map = json.load(f)["weight_map"]
+        except (OSError, KeyError, ValueError) as e:
+            raise CheckpointError(f"read {fn}: {e}") from None
+        self.path = path
+
+    def layer(self, li: int, E: int, H: int, I: int) -> dict:
+        import torch
+        from safetensors import safe_open
+
+        B = FP8_BLOCK
+        if H % B or I % B:
+            raise CheckpointError(f"fp8 experts: hidden {H} / intermediate {I} not a multiple of {B}")
+        prefix = f"model.language_model.layers.{li}.mlp.experts"
+        out = {"gu_q": torch.empty(E, 2 * I, H, dtype=torch.uint8), "gu_s": torch.empty(E, 2 * I // B, H // B),
+               "d_q": torch.empty(E, H, I, dtype=torch.uint8), "d_s": torch.empty(E, H // B, I // B)}
+        handles = {}
+        try:
+            def get(ex, part, scale, rows, cols):
+                name = f"{prefix}.{ex}.{part}.weight" + ("_scale_inv" if scale else "")
+                shard = self.weight_map.get(name)
+                if shard is None:
+                    raise CheckpointError(f"{name} not in the checkpoint index")
+                if shard not in handles:
+                    handles[shard] = safe_open(os.path.join(self.path, shard), framework="pt", device="cpu")
+                f = handles[shard]
+                if name not in f.keys():
+                    raise CheckpointError(f"{name}: not in {shard}")
+                t = f.get_tensor(name)
+                dt, shape = (torch.float32, (rows // B, cols // B)) if scale else (torch.float8_e4m3fn, (rows, cols))
+                if t.dtype != dt or tuple(t.shape) != shape:
+                    raise CheckpointError(f"{name}: {t.dtype} {tuple(t.shape)}, expected {dt} {shape}")
+                return t.view(torch.uint8) if not scale else t
+
+            for ex in range(E):
+                out["gu_q"][ex, :I] = get(ex, "gate_proj", False, I, H)
+                out["gu_q"][ex, I:] = get(ex, "up_proj", False, I, H)
+                out["gu_s"][ex, :I // B] = get(ex, "gate_proj", True, I, H)
+                out["gu_s"][ex, I // B:] = get(ex, "up_proj", True, I, H)
+                out["d_q"][ex] = get(ex, "down_proj", False, H, I)
+                out["d_s"][ex] = get(ex, "down_proj", True, H, I)
+        finally:
+            handles.clear()
+        return out
+
+
 _KEYS = ("router", "nw", "gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")  # dr_decode_layer order
+_EXPERT_KEYS = ("gu_q", "gu_s", "d_q", "d_s")
 
 
 class MoeStack:
-    """The MoE layers of a converted checkpoint resident on the GPU."""
+    """The MoE layers of a converted checkpoint on the GPU.
 
-    def __init__(self, path: str, layers: list[int] | None = None, device: str = "cuda"):
+    With ``fp8_dir`` the routed experts come from the original block-FP8 checkpoint instead
+    of the int4 tensors (the reference's ExpertMode::Fp8, src/model.rs:252-288): layers below
+    ``vram_layers`` (all when None) are uploaded to the GPU, the others stay in pinned host
+    memory that the kernels read over PCIe (src/model.rs:81-97)."""
+
+    def __init__(self, path: str, layers: list[int] | None = None, device: str = "cuda", fp8_dir: str | None = None,
+                 vram_layers: int | None = None):
         import torch
 
         meta = read_meta(path)
@@ -118,8 +192,18 @@ class MoeStack:
         self.H, self.E, self.I = tc["hidden_size"], tc["num_experts"], tc["moe_intermediate_size"]
         self.topk = tc["num_experts_per_tok"]
         self.eps = float(tc.get("rms_norm_eps", 1e-6))
+        self.fp8 = fp8_dir is not None
         ids = list(range(tc["num_hidden_layers"])) if layers is None else list(layers)
-        self.layers = [{k: v.to(device) for k, v in read_layer(path, i, tc).items()} for i in ids]
+        src = Fp8Source(fp8_dir) if self.fp8 else None
+        self.layers = []
+        for i in ids:
+            h = read_layer(path, i, tc, experts=not self.fp8)
+            L = {k: v.to(device) for k, v in h.items()}
+            if src is not None:
+                ex = src.layer(i, self.E, self.H, self.I)
+                on_gpu = vram_layers is None or i < vram_layers
+                L.update({k: (v.to(device) if on_gpu else v.pin_memory()) for k, v in ex.items()})
+            self.layers.append(L)
         tab = [[L[k].data_ptr() for k in _KEYS] for L in self.layers]
         self.table = torch.tensor(tab, dtype=torch.int64, device=device)
         self.ll = torch.zeros(LL_WORDS, dtype=torch.int64, device=device)
@@ -140,9 +224,9 @@ class MoeStack:
     def step(self, x, stream=None, idx_out=None, wts_out=None, sgate_out=None, xs_out=None) -> None:
         """x (f32 [H], device) through every loaded layer in one fused launch, in place."""
         P = dramamoe.ptr
-        self.lib.dr_moe_decode_step(P(self.table), len(self.layers), P(x), self.E, self.H, self.I, self.topk, self.eps,
-                                    P(self.ll), P(self.sync), P(idx_out), P(wts_out), P(sgate_out), P(xs_out),
-                                    stream if stream is not None else dramamoe.stream_ptr())
+        f = self.lib.dr_moe_decode_step_fp8 if self.fp8 else self.lib.dr_moe_decode_step
+        f(P(self.table), len(self.layers), P(x), self.E, self.H, self.I, self.topk, self.eps, P(self.ll), P(self.sync),
+          P(idx_out), P(wts_out), P(sgate_out), P(xs_out), stream if stream is not None else dramamoe.stream_ptr())
         if int(self.sync[1].item()) != 0:
             raise dramamoe.DramaMoeError("dr_moe_decode_step timed out waiting for its workgroups")
 
@@ -198,8 +282,9 @@ class MoeStack:
             lib.dr_moe_topk(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), st)
             lib.dr_moe_group(P(idx), n * k, E, P(counts), P(offsets), P(slot_of), st)
             lib.dr_moe_gather_rows(P(slot_of), n, k, P(hr), P(xp), H, st)
-            lib.dr_moe_prefill(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(xp), P(offsets), P(counts),
-                               P(act), P(yp), E, H, I, st)
+            pf = lib.dr_moe_prefill_fp8 if self.fp8 else lib.dr_moe_prefill
+            pf(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(xp), P(offsets), P(counts), P(act), P(yp), E,
+               H, I, st)
             if overlap:
                 main.wait_event(join)
             lib.dr_moe_combine(P(xr), P(yp), P(slot_of), P(wts), P(sg), P(sh), n, k, H, st)
@@ -220,6 +305,7 @@ class MoeStack:
         for L in self.layers:
             self.lib.dr_router_topk(P(L["router"]), P(x), P(L["nw"]), self.eps, P(logits), self.E, self.topk, self.H,
                                     P(idx), P(wts), P(sg), P(counter), None, None, None, None, 0, 0, 0, 0, st)
-            self.lib.dr_moe_decode(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]),
-                                   P(L["sd_q"]), P(L["sd_s"]), P(x), P(idx), P(wts), P(sg), P(x), P(act), P(x), self.H,
-                                   self.I, self.topk, P(L["nw"]), self.eps, None, 0, st)
+            dec = self.lib.dr_moe_decode_fp8 if self.fp8 else self.lib.dr_moe_decode
+            dec(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]),
+                P(L["sd_s"]), P(x), P(idx), P(wts), P(sg), P(x), P(act), P(x), self.H, self.I, self.topk, P(L["nw"]),
+                self.eps, None, 0, st)

@@ -54,7 +54,9 @@ constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll of
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
-constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + (ST_TOPK + 1) * ST_I, LL_WORDS = LL_X + ST_H;
+// The activation region holds the 4096 routed activations either one fp32 per word (A32) or
+// two 24-bit floats per word, then the 512 shared ones (one fp32 per word).
+constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + ST_TOPK * ST_I + ST_I, LL_WORDS = LL_X + ST_H;
 static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
 static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT, "error codes");
 
@@ -157,44 +159,58 @@ struct Spec32 {
   DEV void post(int, uint64_t) const {}
 };
 
-// activations: words 0..2047 hold routed elements 2w, 2w + 1 (packed, i < 32), words
-// 2048..2559 shared element w - 2048 (one per word, i >= 32); stored into the down slots of
-// the weight format F
-template <class F>
+// activations, routed then shared, stored into the down slots of the weight format F.
+// A32: words 0..4095 hold routed element w (fp32, 32-bit tag), rows i < 64; otherwise words
+// 0..2047 hold routed elements 2w, 2w + 1 as 24-bit floats (16-bit tag), rows i < 32.  The
+// 512 shared elements follow, one fp32 per word, in the last 8 rows.
+template <class F, bool A32>
 struct SpecAct {
+  static constexpr int kRouted = A32 ? 64 : 32, kRows = kRouted + 8, kSharedWord = kRouted * 64;
   uint32_t tag;
   float* dst;   // as4 as floats
   float* sums;  // [0, 128): sums of the 32-element routed chunks (int4), [128, 192): of the 8-element shared chunks
-  DEV bool valid(int r, int) const { return r < 40; }
-  DEV uint64_t ready(int i) const { return i < 32 ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32; }
+  DEV bool valid(int r, int) const { return r < kRows; }
+  DEV uint64_t ready(int i) const {
+    return !A32 && i < kRouted ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32;
+  }
   DEV bool ok(int i, uint64_t v) const {
-    return i < 32 ? (v >> 48) == (tag & 0xffffu) : (uint32_t)(v >> 32) == tag;
+    return !A32 && i < kRouted ? (v >> 48) == (tag & 0xffffu) : (uint32_t)(v >> 32) == tag;
   }
   DEV void store(int i, int w, uint64_t v) const {
-    if (i < 32) {
-      const float2 p = ll_val2(v);
-      float* d = F::act_pair(dst, w);
-      d[0] = p.x, d[1] = p.y;
+    if (i < kRouted) {
+      if constexpr (A32) {
+        F::act_pair(dst, w >> 1)[w & 1] = __uint_as_float((uint32_t)v);
+      } else {
+        const float2 p = ll_val2(v);
+        float* d = F::act_pair(dst, w);
+        d[0] = p.x, d[1] = p.y;
+      }
     } else {
-      const int e = w - 2048;
+      const int e = w - kSharedWord;
       dst[(1024 + ((e >> 2) & 1) * 64 + (e >> 3)) * 4 + (e & 3)] = __uint_as_float((uint32_t)v);
     }
   }
-  // chunk sums for the down dots' min terms: an int4 routed chunk is 16 consecutive words
-  // (lanes) of one row, a shared chunk 8 consecutive words
+  // chunk sums for the down dots' min terms: an int4 routed chunk is 32 (A32) or 16
+  // consecutive words (lanes) of one row, a shared chunk 8 consecutive words
   DEV void post(int r, uint64_t v) const {
     const int lane = lane_id();
-    if (r < 32) {
+    if (r < kRouted) {
       if constexpr (F::kMinTerm) {
-        const float2 p = ll_val2(v);
-        float t = p.x + p.y;
-        t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t);
-        if ((lane & 15) == 0) sums[4 * r + (lane >> 4)] = t;
+        if constexpr (A32) {
+          float t = __uint_as_float((uint32_t)v);
+          t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t), t = xsum_step<16>(t);
+          if ((lane & 31) == 0) sums[2 * r + (lane >> 5)] = t;
+        } else {
+          const float2 p = ll_val2(v);
+          float t = p.x + p.y;
+          t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t), t = xsum_step<8>(t);
+          if ((lane & 15) == 0) sums[4 * r + (lane >> 4)] = t;
+        }
       }
     } else {
       float t = __uint_as_float((uint32_t)v);
       t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
-      if ((lane & 7) == 0) sums[128 + 8 * (r - 32) + (lane >> 3)] = t;
+      if ((lane & 7) == 0) sums[128 + 8 * (r - kRouted) + (lane >> 3)] = t;
     }
   }
 };
@@ -387,7 +403,7 @@ DEV void load_shared_pair(const dr_decode_layer& Ly, int j, int lane, SharedPair
   s.su0 = SH::raw(Ly.sgu_s, I + j, lane * 16, H), s.su1 = SH::raw(Ly.sgu_s, I + j, 1024 + lane * 16, H);
 }
 
-template <class F, class SH>
+template <class F, class SH, bool A32>
 __global__ void __launch_bounds__(ST_NT, 1)
     k_decode_step(const dr_decode_layer* __restrict__ layers, int L, float* x, int E, float eps,
                   uint64_t* __restrict__ ll, uint32_t* __restrict__ sync, int* __restrict__ idx_out,
@@ -511,7 +527,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
         }
         const float gv = wave_sum(SH::cvt(sp.sg0) * (ga - 128.f * sa) + SH::cvt(sp.sg1) * (gb - 128.f * sb));
         const float uv = wave_sum(SH::cvt(sp.su0) * (ua - 128.f * sa) + SH::cvt(sp.su1) * (ub - 128.f * sb));
-        if (lane == 0) ll_put(ll + LL_ACT + ST_TOPK * I / 2 + sj, silu(gv) * uv, tB);
+        if (lane == 0) ll_put(ll + LL_ACT + SpecAct<F, A32>::kSharedWord + sj, silu(gv) * uv, tB);
       }
       ST_MARK(1);
     }
@@ -563,7 +579,14 @@ __global__ void __launch_bounds__(ST_NT, 1)
       {
         float av[2];
         F::gate_up(gu, xq4, s_xsum, lane, av);
-        if (lane == 0) ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
+        if (lane == 0) {
+          if constexpr (A32) {
+            ll_put(ll + LL_ACT + rk * I + rj, av[0], tB);
+            ll_put(ll + LL_ACT + rk * I + rj + 1, av[1], tB);
+          } else {
+            ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
+          }
+        }
       }
       ST_MARK(4);
       // down rows (8 experts + shared): issued after the gate_up stores so the gate_up stream
@@ -578,7 +601,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARKW(14, 2);
       if (poller) {
         ST_MARKW(12, 7);
-        const uint32_t r = poll_wave<5, ST_NP>(ll + LL_ACT, pw, SpecAct<F>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct, tmo);
+        const uint32_t r = poll_wave<SpecAct<F, A32>::kRows / ST_NP, ST_NP>(
+            ll + LL_ACT, pw, SpecAct<F, A32>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct, tmo);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -670,19 +694,31 @@ int step_grid_ok(const void* kernel) {
 
 std::atomic<uint64_t> g_wait_ticks{ST_TIMEOUT_TICKS};
 
+// Transport of the routed activations: fp32 (default) or 24-bit floats (half the words);
+// dr_step_set_act_exchange selects it for later launches.
+std::atomic<int> g_act_bits{32};
+
+template <class F, class SH, bool A32>
+int launch_step_as(const dr_decode_layer* layers, int L, float* x, int E, float eps, uint64_t* ll, uint32_t* sync,
+                   int* idx_out, float* wts_out, float* sgate_out, float* xs_out, hipStream_t st) {
+  const void* k = reinterpret_cast<const void*>(&k_decode_step<F, SH, A32>);
+  if (!step_grid_ok(k)) return -1;
+  uint32_t* err = err_word();
+  if (err_pending() == DR_ERR_STEP_TIMEOUT) return DR_ERR_STEP_TIMEOUT;  // until dr_last_error clears it
+  hipLaunchKernelGGL((k_decode_step<F, SH, A32>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
+                     idx_out, wts_out, sgate_out, xs_out, err, g_wait_ticks.load(std::memory_order_relaxed));
+  return 0;
+}
+
 template <class F, class SH>
 int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, int I, int topk, float eps,
                 uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out, float* xs_out,
                 hipStream_t st) {
   if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || L < 1 || L > ST_MAXL) return -1;
   if (!layers || !x || !ll || !sync) return -1;
-  const void* k = reinterpret_cast<const void*>(&k_decode_step<F, SH>);
-  if (!step_grid_ok(k)) return -1;
-  uint32_t* err = err_word();
-  if (err_pending() == DR_ERR_STEP_TIMEOUT) return DR_ERR_STEP_TIMEOUT;  // until dr_last_error clears it
-  hipLaunchKernelGGL((k_decode_step<F, SH>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
-                     idx_out, wts_out, sgate_out, xs_out, err, g_wait_ticks.load(std::memory_order_relaxed));
-  return 0;
+  if (g_act_bits.load(std::memory_order_relaxed) == 24)
+    return launch_step_as<F, SH, false>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
+  return launch_step_as<F, SH, true>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
 }
 
 constexpr int ST_SCRATCH_WORDS = LL_WORDS + 2;  // ll, then sync[4] as two 64-bit words
@@ -735,6 +771,12 @@ API int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_la
   return launch_step<StepQ4<ScaleBF16>, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, p,
                                                    reinterpret_cast<uint32_t*>(p + LL_WORDS), idx_out, wts_out,
                                                    sgate_out, xs_out, (hipStream_t)st);
+}
+
+API int dr_step_set_act_exchange(int bits) {
+  if (bits != 32 && bits != 24) return -1;
+  g_act_bits.store(bits, std::memory_order_relaxed);
+  return 0;
 }
 
 API int dr_step_set_wait_limit(uint32_t us) {

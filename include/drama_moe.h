@@ -269,6 +269,12 @@ int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, in
 int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                              int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                              float* sgate_out, float* xs_out, dr_stream_t st);
+/* Transport of the routed activations between the fused step's workgroups, for later launches:
+ * 32 (default) carries them as fp32, like the reference's act buffer (kernels/drama.cu:493,516);
+ * 24 packs two 24-bit floats (15-bit mantissa, relative error <= 2^-16) per slot, half the
+ * exchange traffic.  Other values -> -1. */
+int dr_step_set_act_exchange(int bits);
+
 /* Wait limit of the fused step's exchanges in microseconds (0 restores the default, 200000).
  * A call whose workgroups are not all resident within the limit (another kernel holding CUs)
  * gives up: x becomes NaN, sync[1] is set and DR_ERR_STEP_TIMEOUT is raised.  For tests that

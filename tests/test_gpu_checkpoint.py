@@ -82,3 +82,66 @@ def test_checkpoint_prefill_chunked(tmp_path):
     err = np.abs(got - ref) - 5e-3 * (1 + np.abs(ref))
     assert (err > 0).mean() <= 1e-4, f"prefill vs oracle: {int((err > 0).sum())} elements beyond 5e-3"
     assert_close(got, ref, rtol=5e-2, atol=5e-2, what="prefill vs oracle")
+
+
+def test_checkpoint_fp8_source_step_chain_prefill(tmp_path):
+    """Routed experts from the original block-FP8 checkpoint (Fp8Source) beside the converted
+    router/shared tensors: layer 0 on the GPU, layer 1 in pinned host memory read over PCIe
+    (vram_layers=1).  Fused step: routing bit-exact with the oracle per layer, outputs within
+    1e-3 + 1e-3 |ref|; the per-layer chain agrees with the step; prefill runs the FP8
+    grouped kernels."""
+    import torch
+
+    import synth
+    from ckpt_helpers import write_fp8_source
+
+    E, H, I = 16, 2048, 512
+    conv = tmp_path / "conv"
+    src = tmp_path / "fp8"
+    conv.mkdir()
+    src.mkdir()
+    layers = write_checkpoint(conv, [70, 71], E=E)
+    fp8 = [synth.make_layer(80 + i, E=E, fmt="ref", kind="fp8", quick=True) for i in range(2)]
+    write_fp8_source(str(src), fp8, E)
+    st = C.MoeStack(str(conv), fp8_dir=str(src), vram_layers=1)
+    assert st.layers[0]["gu_q"].is_cuda and not st.layers[1]["gu_q"].is_cuda and st.layers[1]["gu_q"].is_pinned()
+    oracle_layers = []
+    for L, F in zip(layers, fp8):
+        M = dict(L)
+        M.update({k: F[k] for k in ("kind", "gu_q", "gu_s", "d_q", "d_s", "sc_kind")})
+        oracle_layers.append(M)
+    n = 2
+    x0 = np.random.default_rng(7).normal(0, 1, H).astype(np.float32)
+    idx = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
+    wts = torch.zeros(n * 8, device="cuda")
+    xs = torch.zeros(n * H, device="cuda")
+    xd = dev(x0)
+    st.step(xd, idx_out=idx, wts_out=wts, xs_out=xs)
+    torch.cuda.synchronize()
+    gi, gw, gx = host(idx).reshape(n, 8), host(wts).reshape(n, 8), host(xs).reshape(n, H)
+    xin = x0
+    for l, L in enumerate(oracle_layers):
+        _, ri, rw, rs = O.router_topk(L["router"], xin, L["nw"], 1e-6, E, 8)
+        np.testing.assert_array_equal(gi[l], ri)
+        np.testing.assert_array_equal(bits(gw[l]), bits(rw))
+        _, ry = O.moe_decode(L, xin, ri, rw, rs, xin, H, I, 8, nw=L["nw"], eps=1e-6)
+        assert_close(gx[l], ry, what=f"fp8 layer {l}")
+        xin = gx[l].copy()
+    xc = dev(x0)
+    st.chain(xc)
+    torch.cuda.synchronize()
+    assert_close(host(xc), gx[-1], what="fp8 chain vs fused step")
+    rows = 24
+    rng = np.random.default_rng(8)
+    hn = synth.f32_to_bf16(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    xp0 = rng.normal(0, 1, (rows, H)).astype(np.float32)
+    xa, dhn = dev(xp0), dev(hn)
+    st.prefill(0, xa.view(rows, H), dhn.view(rows, H))
+    torch.cuda.synchronize()
+    L = oracle_layers[0]
+    rl = O.router_logits_rows(hn, L["router"], rows, E + 1, H)
+    ri, rw, rs = O.moe_topk(rl, rows, E, 8, E + 1)
+    ref = O.moe_prefill_layer(L, hn, rows, ri, rw, rs, xp0, H, I, 8)
+    got = host(xa).reshape(rows, H).astype(np.float64)
+    err = np.abs(got - ref) - 5e-3 * (1 + np.abs(ref))
+    assert (err > 0).mean() <= 1e-4, f"fp8 prefill vs oracle: {int((err > 0).sum())} elements beyond 5e-3"

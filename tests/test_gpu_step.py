@@ -64,25 +64,38 @@ def check_stack(st, x0, idx, wts, sg, xs, x_final):
     np.testing.assert_array_equal(bits(x_final), bits(xs[-1]))
 
 
-@pytest.mark.parametrize("fmt,E,n", [("cfg", 256, 3), ("ref", 256, 2), ("cfg", 64, 4), ("cfg", 8, 2)])
-def test_step_matches_oracle_layer_by_layer(fmt, E, n):
-    print(f"step parity fmt={fmt} E={E} layers={n}", flush=True)
+@pytest.mark.parametrize("fmt,E,n,bits", [("cfg", 256, 3, 32), ("ref", 256, 2, 32), ("cfg", 64, 4, 32), ("cfg", 8, 2, 32),
+                                          ("cfg", 256, 3, 24), ("ref", 64, 2, 24)])
+def test_step_matches_oracle_layer_by_layer(fmt, E, n, bits):
+    """bits: transport of the routed activations between workgroups (fp32, or 24-bit floats)."""
+    print(f"step parity fmt={fmt} E={E} layers={n} act exchange {bits} bit", flush=True)
     st = Stack([300 + 7 * i for i in range(n)], E, fmt)
     x0 = np.random.default_rng(5).normal(0, 1, H).astype(np.float32)
     xd = dev(x0)
-    idx, wts, sg, xs = st.run(xd)
+    L = D.lib()
+    L.dr_step_set_act_exchange(bits)
+    try:
+        idx, wts, sg, xs = st.run(xd)
+    finally:
+        L.dr_step_set_act_exchange(32)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"
     check_stack(st, x0, idx, wts, sg, xs, host(xd))
 
 
-@pytest.mark.parametrize("fmt,E,n", [("cfg", 32, 3), ("ref", 16, 2), ("cfg", 8, 2), ("cfg", 16, 1)])
-def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n):
+@pytest.mark.parametrize("fmt,E,n,bits", [("cfg", 32, 3, 32), ("ref", 16, 2, 32), ("cfg", 8, 2, 32), ("cfg", 16, 1, 32),
+                                          ("cfg", 32, 2, 24)])
+def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n, bits):
     """Block-FP8 routed experts (dr_moe_decode_step_fp8*): the same routing and layer bar."""
-    print(f"fp8 step parity fmt={fmt} E={E} layers={n}", flush=True)
+    print(f"fp8 step parity fmt={fmt} E={E} layers={n} act exchange {bits} bit", flush=True)
     st = Stack([500 + 3 * i for i in range(n)], E, fmt, kind="fp8")
     x0 = np.random.default_rng(15).normal(0, 1, H).astype(np.float32)
     xd = dev(x0)
-    idx, wts, sg, xs = st.run(xd)
+    L = D.lib()
+    L.dr_step_set_act_exchange(bits)
+    try:
+        idx, wts, sg, xs = st.run(xd)
+    finally:
+        L.dr_step_set_act_exchange(32)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"
     check_stack(st, x0, idx, wts, sg, xs, host(xd))
 
@@ -138,6 +151,7 @@ def test_step_without_norm_and_without_outputs(kind):
 
 
 def test_step_rejects_bad_shapes():
+    assert D.lib().raw("dr_step_set_act_exchange")(16) == -1
     st = Stack([1], 16, "cfg")
     x = dev(np.zeros(H, np.float32))
     L = D.lib()

@@ -290,8 +290,31 @@ def config5_fp8(lib, st, iters=100, copies=4):
     ms4 = timed(b4, iters, st)
     ms4g = timed_graph(b4, iters, st, copies)
     nb4, hit = pf.layer_bytes(L)
-    out["decode_batch4"] = rec(ms4 * 1000, nb4, experts_hit=hit, us_graph=round(ms4g * 1000, 2),
-                               note="4 rows via the grouped MFMA path (bf16 act); us_graph: replayed from a HIP graph")
+    out["decode_batch4_grouped"] = rec(ms4 * 1000, nb4, experts_hit=hit, us_graph=round(ms4g * 1000, 2),
+                                       note="4 rows via the prefill path (router GEMM, top-k, grouping, gather, "
+                                            "grouped MFMA GEMM, combine: 9 launches); us_graph: from a HIP graph")
+    # the small-batch decode path: router + top-k for the 4 rows in one launch, then the batch-1
+    # chain's expert kernels over the 4 rows (3 launches)
+    x4 = torch.randn(4, H, device="cuda")
+    lg4, idx4, wts4, sg4 = z(4 * (E + 1)), z(4 * TOPK, torch.int32), z(4 * TOPK), z(4)
+    act4 = z(4 * 9 * I)
+
+    def b4r(i):
+        Lc = Ls[i % copies]
+        lib.dr_router_topk_rows(P(Lc["router"]), P(x4), P(Lc["nw"]), 1e-6, P(lg4), E, TOPK, H, 4, P(idx4), P(wts4),
+                                P(sg4), P(counter), sp)
+        lib.dr_moe_decode_rows_fp8_bf16s(P(Lc["gu_q"]), P(Lc["gu_s"]), P(Lc["d_q"]), P(Lc["d_s"]), P(Lc["sgu_q"]),
+                                         P(Lc["sgu_s"]), P(Lc["sd_q"]), P(Lc["sd_s"]), P(x4), P(idx4), P(wts4), P(sg4),
+                                         P(x4), P(act4), P(x4), None, 4, H, I, TOPK, P(Lc["nw"]), 1e-6, sp)
+
+    ms4r = timed(b4r, iters, st)
+    ms4rg = timed_graph(b4r, iters, st, copies)
+    hit4 = int(torch.unique(idx4).numel())
+    nb4r = (L["router"].numel() * 2 + hit4 * per_expert + shared + 4 * 6 * H * 4 + 4 * 2 * 9 * I * 4)
+    out["decode_batch4"] = rec(ms4r * 1000, nb4r, experts_hit=hit4, us_graph=round(ms4rg * 1000, 2),
+                               note="4 rows via the small-batch decode path (dr_router_topk_rows + "
+                                    "dr_moe_decode_rows_fp8_bf16s, 3 launches); bytes = router + distinct "
+                                    "experts + shared + vectors; us_graph: replayed from a HIP graph")
     del L, Ls, routers
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections

@@ -45,6 +45,13 @@ DEV uint2 ld8(const void* p) {
   const gu32x2 v = gld<gu32x2>(p);
   return make_uint2(v.x, v.y);
 }
+// Keeps the loads issued before this point ahead of those issued after it (a compiler memory
+// barrier, which also stops loads from being sunk towards their first use, and a scheduling
+// barrier).  A wave's loads return in order, so staging loads issued first do not wait for
+// the weight loads behind them.
+DEV void issue_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+}
 DEV float4 ldf4(const void* p) {
   const gu32x4 v = gld<gu32x4>(p);
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));

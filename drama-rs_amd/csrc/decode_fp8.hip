@@ -8,6 +8,8 @@
 //            int8 shared row.
 // One scale per 128 x 128 block (f32 scale_inv in the reference layout, bf16 in the
 // benchmark configuration); every 16-element lane chunk lies inside one block.
+#include <type_traits>
+
 #include "common.hpp"
 
 using namespace drm;
@@ -15,10 +17,6 @@ using namespace drm;
 namespace {
 
 constexpr int H8 = 2048, I8 = 512, TOPK8 = 8;
-constexpr int G8_WPB = 4, G8_PPW = 1;  // gate_up: waves per block, (gate, up) pairs per wave
-constexpr int G8_NB_ROUTED = TOPK8 * I8 / (G8_WPB * G8_PPW);
-constexpr int G8_NB_SHARED = I8 / G8_WPB;
-constexpr int D8_WPB = 4, D8_RPW = 2;
 
 DEV float dot16_u8b(const uint4& w, const float* x, float acc) {
   acc = dot4_u8b(w.x, x, acc);
@@ -27,74 +25,79 @@ DEV float dot16_u8b(const uint4& w, const float* x, float acc) {
   return dot4_u8b(w.w, x + 12, acc);
 }
 
-template <int H>
-DEV void stage_xn16(const float* __restrict__ x, const float* __restrict__ nw, float eps, float4* xs) {
-  __shared__ float red[4];
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  constexpr int PER = H / 4 / 256;
-  float4 v[PER], w[PER];
+// Stage NR rows of RMSNorm(x) (nw == nullptr: x itself) in LDS for the 16-element lane chunks
+// of the 2048-wide rows: float4 f of a row goes to lane (f & 255) >> 2 of part f >> 8, slot
+// f & 3.  load() issues the global loads unconditionally and ahead of everything issued after
+// it (loads return in order, so weight loads issued later do not delay the staging);
+// finish() reduces (partial sums added in wave order), normalises and writes LDS.  Every
+// thread of the block calls both.
+template <int H, int NT, int NR>
+struct XStage {
+  static constexpr int NWV = NT / WAVE, PER = H / 4 / NT;
+  float4 v[NR][PER], w[PER];
+  DEV void load(const float* x, const float* nw) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* n4 = reinterpret_cast<const float4*>(nw ? nw : x);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) v[i] = x4[threadIdx.x + 256 * i];
-  if (nw) {
-    const float4* n4 = reinterpret_cast<const float4*>(nw);
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
-    for (int i = 0; i < PER; ++i) w[i] = n4[threadIdx.x + 256 * i];
-    float ss = 0.f;
+      for (int i = 0; i < PER; ++i) v[r][i] = ldf4(x4 + r * (H / 4) + threadIdx.x + NT * i);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    ss = wave_sum(ss);
-    if (lane_id() == 0) red[wave_id()] = ss;
+    for (int i = 0; i < PER; ++i) w[i] = ldf4(n4 + threadIdx.x + NT * i);
+    issue_fence();
+  }
+  DEV void finish(bool norm, float eps, float4* xs) {
+    __shared__ float red[NR][NWV];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        ss += v[r][i].x * v[r][i].x + v[r][i].y * v[r][i].y + v[r][i].z * v[r][i].z + v[r][i].w * v[r][i].w;
+      ss = wave_sum(ss);
+      if (lane_id() == 0) red[r][wave_id()] = ss;
+    }
     __syncthreads();
-    const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      v[i] = make_float4(v[i].x * inv * w[i].x, v[i].y * inv * w[i].y, v[i].z * inv * w[i].z, v[i].w * inv * w[i].w);
-  }
-  // float4 f -> lane (f & 255) >> 2 of part f >> 8, slot i = f & 3
+    for (int r = 0; r < NR; ++r) {
+      float t = red[r][0];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int f = threadIdx.x + 256 * i;
-    xs[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = v[i];
+      for (int q = 1; q < NWV; ++q) t += red[r][q];
+      // without a norm weight: x * 1 * 1 == x exactly
+      const float inv = norm ? rsqrtf(t / (float)H + eps) : 1.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const float wx = norm ? w[i].x : 1.f, wy = norm ? w[i].y : 1.f, wz = norm ? w[i].z : 1.f,
+                    ww = norm ? w[i].w : 1.f;
+        v[r][i] = make_float4(v[r][i].x * inv * wx, v[r][i].y * inv * wy, v[r][i].z * inv * wz, v[r][i].w * inv * ww);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int f = threadIdx.x + NT * i;
+        xs[r * (H / 4) + (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = v[r][i];
+      }
+    __syncthreads();
   }
-  __syncthreads();
+};
+
+// Keeps the weight registers opaque until this point, so the compiler cannot convert them to
+// float ahead of the x staging (PPW pairs expanded to fp32 would need 64 PPW registers).
+DEV void opaque(uint4& w) {
+  uint32_t a = w.x, b = w.y, c = w.z, d = w.w;
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  w = make_uint4(a, b, c, d);
+}
+template <int PPW>
+DEV void pin_weights(uint4 (&g0)[PPW], uint4 (&g1)[PPW], uint4 (&u0)[PPW], uint4 (&u1)[PPW]) {
+#pragma unroll
+  for (int p = 0; p < PPW; ++p) opaque(g0[p]), opaque(g1[p]), opaque(u0[p]), opaque(u1[p]);
 }
 
-template <int SF, class SH>
-__global__ void __launch_bounds__(256)
-    k_moe_gate_up_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
-                      const uint16_t* __restrict__ shs, const float* __restrict__ x, const int* __restrict__ idx,
-                      float* __restrict__ act, const float* __restrict__ nw, float eps) {
-  constexpr int H = H8, I = I8;
-  __shared__ float4 xs[H / 4];
-  const int lane = lane_id(), wave = wave_id();
-  const bool routed = blockIdx.x < G8_NB_ROUTED;
-  int k, j;
-  const uint8_t *rg, *ru;
-  float sg0, sg1, su0, su1;
-  if (routed) {
-    constexpr int BPE = G8_NB_ROUTED / TOPK8;
-    k = blockIdx.x / BPE;
-    j = (blockIdx.x % BPE) * G8_WPB + wave;
-    const size_t e = (size_t)idx[k];
-    const uint8_t* w = W + e * (2 * I) * H;
-    rg = w + (size_t)j * H + lane * 16;
-    ru = w + (size_t)(I + j) * H + lane * 16;
-    const size_t sb = e * (size_t)(2 * I / 128) * (H / 128);
-    sg0 = blk_scale<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + (lane >> 3));
-    sg1 = blk_scale<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + 8 + (lane >> 3));
-    su0 = blk_scale<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + (lane >> 3));
-    su1 = blk_scale<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + 8 + (lane >> 3));
-  } else {
-    k = TOPK8;
-    j = (blockIdx.x - G8_NB_ROUTED) * G8_WPB + wave;
-    rg = reinterpret_cast<const uint8_t*>(shq) + (size_t)j * H + lane * 16;
-    ru = reinterpret_cast<const uint8_t*>(shq) + (size_t)(I + j) * H + lane * 16;
-    sg0 = SH::scale(shs, j, lane * 16, H), sg1 = SH::scale(shs, j, 1024 + lane * 16, H);
-    su0 = SH::scale(shs, I + j, lane * 16, H), su1 = SH::scale(shs, I + j, 1024 + lane * 16, H);
-  }
-  const uint4 g0 = ld16(rg), g1 = ld16(rg + 1024), u0 = ld16(ru), u1 = ld16(ru + 1024);
-  stage_xn16<H>(x, nw, eps, xs);
-  float xa[16], xb[16], sa = 0.f, sb = 0.f;
+DEV void unpack16(const float4* xs, int lane, float (&xa)[16], float (&xb)[16], float& sa, float& sb) {
+  sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float4 v = xs[i * 64 + lane], w = xs[256 + i * 64 + lane];
@@ -103,60 +106,157 @@ __global__ void __launch_bounds__(256)
     sa += (v.x + v.y) + (v.z + v.w);
     sb += (w.x + w.y) + (w.z + w.w);
   }
-  float g, u;
-  if (routed) {
-    g = sg0 * dot16_fp8(g0, xa, 0.f) + sg1 * dot16_fp8(g1, xb, 0.f);
-    u = su0 * dot16_fp8(u0, xa, 0.f) + su1 * dot16_fp8(u1, xb, 0.f);
-  } else {
-    g = sg0 * (dot16_u8b(g0, xa, 0.f) - 128.f * sa) + sg1 * (dot16_u8b(g1, xb, 0.f) - 128.f * sb);
-    u = su0 * (dot16_u8b(u0, xa, 0.f) - 128.f * sa) + su1 * (dot16_u8b(u1, xb, 0.f) - 128.f * sb);
-  }
-  g = wave_sum(g);
-  u = wave_sum(u);
-  if (lane == 0) act[k * I + j] = silu(g) * u;
 }
 
-template <int SF, class SH>
-__global__ void __launch_bounds__(256)
+// gate_up of B decode rows.  Routed units are (row b, pick k, pair j), j fastest; the NBR
+// routed blocks' waves walk them spaced by the grid (wave g takes units g, g + NW, ..., so
+// waves running side by side read neighbouring rows of one expert), keeping D units in flight
+// and loading unit p + D once unit p is computed.  The shared-expert blocks that follow (PPWS
+// pairs per wave, all loaded at once) serve all B rows with one read of their weights.  x
+// (and the norm weight) are requested before the weights, so the staging overlaps the fetch.
+template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B>
+__global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 1)))
+    k_moe_gate_up_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
+                      const uint16_t* __restrict__ shs, const float* x, const int* __restrict__ idx,
+                      float* __restrict__ act, const float* nw, float eps) {
+  constexpr int H = H8, I = I8, NT = WPB * 64, NW = NBR * WPB, PPW = B * TOPK8 * I / NW;
+  static_assert(PPW * NW == B * TOPK8 * I && D <= PPW, "units split evenly over the routed waves");
+  constexpr int NBS = I / (WPB * PPWS);  // shared-expert blocks, dispatched first
+  const int lane = lane_id(), wave = wave_id();
+  __shared__ float4 xs[B * H / 4];
+  if ((int)blockIdx.x >= NBS) {
+    const int g = (blockIdx.x - NBS) * WPB + wave;
+    XStage<H, NT, B> xst;
+    xst.load(x, nw);
+    uint4 g0[D], g1[D], u0[D], u1[D];
+    uint32_t sr[D][4];
+    auto issue = [&](int p, int d) {
+      const int u = g + NW * p, b = u / (TOPK8 * I), k = (u / I) % TOPK8, j = u % I;
+      const size_t e = (size_t)idx[b * TOPK8 + k];
+      const uint8_t* rg = W + (e * (2 * I) + j) * H + lane * 16;
+      const uint8_t* ru = rg + (size_t)I * H;
+      g0[d] = ld16(rg), g1[d] = ld16(rg + 1024), u0[d] = ld16(ru), u1[d] = ld16(ru + 1024);
+      const size_t sb = e * (size_t)(2 * I / 128) * (H / 128);
+      sr[d][0] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + (lane >> 3));
+      sr[d][1] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + 8 + (lane >> 3));
+      sr[d][2] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + (lane >> 3));
+      sr[d][3] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + 8 + (lane >> 3));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int p = 0; p < D; ++p) issue(p, p);
+    xst.finish(nw != nullptr, eps, xs);
+#pragma unroll
+    for (int p = 0; p < PPW; ++p) {
+      const int d = p % D;
+      const int u = g + NW * p, b = u / (TOPK8 * I), k = (u / I) % TOPK8, j = u % I;
+      float xa[16], xb[16], sa, sbm;
+      unpack16(xs + b * (H / 4), lane, xa, xb, sa, sbm);
+      opaque(g0[d]), opaque(g1[d]), opaque(u0[d]), opaque(u1[d]);
+      float gv = blk_cvt<SF>(sr[d][0]) * dot16_fp8(g0[d], xa, 0.f) + blk_cvt<SF>(sr[d][1]) * dot16_fp8(g1[d], xb, 0.f);
+      float uv = blk_cvt<SF>(sr[d][2]) * dot16_fp8(u0[d], xa, 0.f) + blk_cvt<SF>(sr[d][3]) * dot16_fp8(u1[d], xb, 0.f);
+      if (p + D < PPW) issue(p + D, d);
+      gv = wave_sum(gv);
+      uv = wave_sum(uv);
+      if (lane == 0) act[(size_t)b * (TOPK8 + 1) * I + k * I + j] = silu(gv) * uv;
+    }
+  } else {
+    const int j0 = (blockIdx.x * WPB + wave) * PPWS;
+    XStage<H, NT, B> xst;
+    xst.load(x, nw);
+    uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
+    float sg0[PPWS], sg1[PPWS], su0[PPWS], su1[PPWS];
+#pragma unroll
+    for (int p = 0; p < PPWS; ++p) {
+      const uint8_t* rg = reinterpret_cast<const uint8_t*>(shq) + (size_t)(j0 + p) * H + lane * 16;
+      const uint8_t* ru = reinterpret_cast<const uint8_t*>(shq) + (size_t)(I + j0 + p) * H + lane * 16;
+      g0[p] = ld16(rg), g1[p] = ld16(rg + 1024), u0[p] = ld16(ru), u1[p] = ld16(ru + 1024);
+    }
+#pragma unroll
+    for (int p = 0; p < PPWS; ++p) {
+      const int j = j0 + p;
+      sg0[p] = SH::scale(shs, j, lane * 16, H), sg1[p] = SH::scale(shs, j, 1024 + lane * 16, H);
+      su0[p] = SH::scale(shs, I + j, lane * 16, H), su1[p] = SH::scale(shs, I + j, 1024 + lane * 16, H);
+    }
+    xst.finish(nw != nullptr, eps, xs);
+#pragma unroll 1
+    for (int r = 0; r < B; ++r) {
+      pin_weights(g0, g1, u0, u1);  // converted per row, not hoisted out of the row loop
+      float xa[16], xb[16], sa, sbm;
+      unpack16(xs + r * (H / 4), lane, xa, xb, sa, sbm);
+      float* ar = act + (size_t)r * (TOPK8 + 1) * I + TOPK8 * I + j0;
+#pragma unroll
+      for (int p = 0; p < PPWS; ++p) {
+        float g = sg0[p] * (dot16_u8b(g0[p], xa, 0.f) - 128.f * sa) + sg1[p] * (dot16_u8b(g1[p], xb, 0.f) - 128.f * sbm);
+        float u = su0[p] * (dot16_u8b(u0[p], xa, 0.f) - 128.f * sa) + su1[p] * (dot16_u8b(u1[p], xb, 0.f) - 128.f * sbm);
+        g = wave_sum(g);
+        u = wave_sum(u);
+        if (lane == 0) ar[p] = silu(g) * u;
+      }
+    }
+  }
+}
+
+// down of decode row blockIdx.y: wave w of block b owns output rows n0 .. n0 + RPW - 1 and
+// gathers, per row, the 8 routed expert rows of 512 bytes (load i: experts 2 i on lanes 0-31,
+// 2 i + 1 on lanes 32-63) and 8 bytes of the int8 shared row per lane; the row's activations
+// are staged in LDS.
+template <int SF, class SH, int WPB, int RPW>
+__global__ void __launch_bounds__(WPB * 64)
     k_moe_down_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
-                   const uint16_t* __restrict__ shs, const float* __restrict__ act, const int* __restrict__ idx,
+                   const uint16_t* __restrict__ shs, const float* act, const int* __restrict__ idx,
                    const float* __restrict__ wts, const float* __restrict__ sgate, const float* res, float* y,
                    uint16_t* yb, const char* pf, size_t pf_bytes) {
-  constexpr int H = H8, I = I8;
-  __shared__ float4 as[(TOPK8 + 1) * I / 4];
+  constexpr int H = H8, I = I8, AW = (TOPK8 + 1) * I / 4, NT = WPB * 64;
+  __shared__ float4 as[AW];
   const int lane = lane_id(), wave = wave_id();
-  const int half = lane >> 5, cc = lane & 31;
+  const int half = lane >> 5, cc = lane & 31, b = blockIdx.y;
+  const int n0 = (blockIdx.x * WPB + wave) * RPW;
+  act += (size_t)b * (TOPK8 + 1) * I, idx += b * TOPK8, wts += b * TOPK8;
+  // pick indices with scalar loads, then the activations (requested before the weights, so
+  // the staging overlaps the weight fetch), then the weights row by row
   size_t e[4];
   float w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) e[i] = (size_t)idx[2 * i + half], w[i] = wts[2 * i + half];
-  const int n0 = (blockIdx.x * D8_WPB + wave) * D8_RPW;
-  uint4 q[D8_RPW][4];
-  float sc[D8_RPW][4];
-  uint2 qs[D8_RPW];
-  float ss[D8_RPW];
+  for (int i = 0; i < 4; ++i) {
+    const int ea = idx[2 * i], eb = idx[2 * i + 1];
+    const float wa = wts[2 * i], wb = wts[2 * i + 1];
+    e[i] = (size_t)(half ? eb : ea);
+    w[i] = half ? wb : wa;
+  }
+  const float sgv = sigmoid(sgate[b]);
+  constexpr int NA = 1024 / NT;
+  const float4* a4 = reinterpret_cast<const float4*>(act);
+  float4 av[NA + 1];
 #pragma unroll
-  for (int r = 0; r < D8_RPW; ++r) {
+  for (int t = 0; t < NA; ++t) av[t] = ldf4(a4 + threadIdx.x + NT * t);
+  av[NA] = ldf4(a4 + 1024 + (threadIdx.x & 127));
+  issue_fence();
+  uint4 q[RPW][4];
+  uint32_t sc[RPW][4];
+  uint2 qs[RPW];
+  uint32_t ssr[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
     const size_t n = (size_t)(n0 + r);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       q[r][i] = ld16(W + (e[i] * H + n) * I + cc * 16);
-      sc[r][i] = blk_scale<SF>(S, (e[i] * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
+      sc[r][i] = blk_raw<SF>(S, (e[i] * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
     }
     qs[r] = ld8(shq + n * I + lane * 8);
-    ss[r] = SH::scale(shs, n, lane * 8, I);
+    ssr[r] = SH::raw(shs, n, lane * 8, I);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  const float sgv = sigmoid(sgate[0]);
   // routed act: lane slice of load i = act[1024 i + 16 l .. + 16) -> 4 float4 per part of 256
-  const float4* a4 = reinterpret_cast<const float4*>(act);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = threadIdx.x + 256 * i;
-    as[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = a4[f];
+  for (int t = 0; t < NA; ++t) {
+    const int f = threadIdx.x + NT * t;
+    as[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = av[t];
   }
-  if (threadIdx.x < 128) {
+  if ((int)threadIdx.x < 128) {
     const int f = threadIdx.x;
-    as[1024 + (f & 1) * 64 + (f >> 1)] = a4[1024 + f];
+    as[1024 + (f & 1) * 64 + (f >> 1)] = av[NA];
   }
   __syncthreads();
   float xa[4][16], xc[8], sumc = 0.f;
@@ -174,15 +274,15 @@ __global__ void __launch_bounds__(256)
     sumc += (v.x + v.y) + (v.z + v.w);
   }
 #pragma unroll
-  for (int r = 0; r < D8_RPW; ++r) {
+  for (int r = 0; r < RPW; ++r) {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc += w[i] * sc[r][i] * dot16_fp8(q[r][i], xa[i], 0.f);
+    for (int i = 0; i < 4; ++i) acc += w[i] * blk_cvt<SF>(sc[r][i]) * dot16_fp8(q[r][i], xa[i], 0.f);
     float dc = dot4_u8b(qs[r].x, xc, 0.f);
     dc = dot4_u8b(qs[r].y, xc + 4, dc);
-    acc += sgv * ss[r] * (dc - 128.f * sumc);
+    acc += sgv * SH::cvt(ssr[r]) * (dc - 128.f * sumc);
     acc = wave_sum(acc);
-    const int n = n0 + r;
+    const size_t n = (size_t)b * H + n0 + r;
     if (lane == 0) {
       const float out = res[n] + acc;
       y[n] = out;
@@ -192,16 +292,48 @@ __global__ void __launch_bounds__(256)
   warm_range(pf, pf_bytes);
 }
 
+// Launch shapes: batch 1 (the engine's per-layer chain) uses small blocks, many of them.
+// B > 1 uses 512-thread blocks, two per CU: gate_up walks B * 8 * 512 / 4096 units per wave
+// with 2 in flight (measured at B = 4: 37.8 us for the three launches, against 39.1 with one
+// block of 3 in flight per CU and 43.0 with 4 in flight, whose registers spill).
+template <int SF, class SH, int B>
+void launch_decode_fp8_b(const uint8_t* gu_w, const void* gu_s, const uint8_t* d_w, const void* d_s,
+                         const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                         const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                         float* act, float* y, uint16_t* yb, const float* nw, float eps, const char* pf,
+                         size_t pf_bytes, hipStream_t st) {
+  constexpr int GW = B == 1 ? 4 : 8, GB = B == 1 ? 1024 : 512, GD = B == 1 ? 1 : 2;
+  constexpr int GS = B == 1 ? 1 : 2, DW = B == 1 ? 4 : 8, DR = 2;
+  constexpr int NB = GB + I8 / (GW * GS);
+  hipLaunchKernelGGL((k_moe_gate_up_fp8<SF, SH, GW, GB, GD, GS, B>), dim3(NB), dim3(GW * 64), 0, st, gu_w, gu_s, sgu_q,
+                     sgu_s, x, idx, act, nw, eps);
+  hipLaunchKernelGGL((k_moe_down_fp8<SF, SH, DW, DR>), dim3(H8 / (DW * DR), B), dim3(DW * 64), 0, st, d_w, d_s, sd_q,
+                     sd_s, act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
+}
+
+// rows independent decode rows (x, res, y: [rows, H]; idx, wts: [rows, topk]; act: rows x
+// (topk + 1) x I), launched 4 rows at a time
 template <int SF, class SH>
 int launch_decode_fp8(const uint8_t* gu_w, const void* gu_s, const uint8_t* d_w, const void* d_s, const int8_t* sgu_q,
                       const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s, const float* x, const int* idx,
                       const float* wts, const float* sgate, const float* res, float* act, float* y, uint16_t* yb, int H,
-                      int I, int topk, const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st) {
-  if (H != H8 || I != I8 || topk != TOPK8) return -1;
-  hipLaunchKernelGGL((k_moe_gate_up_fp8<SF, SH>), dim3(G8_NB_ROUTED + G8_NB_SHARED), dim3(256), 0, st, gu_w, gu_s,
-                     sgu_q, sgu_s, x, idx, act, nw, eps);
-  hipLaunchKernelGGL((k_moe_down_fp8<SF, SH>), dim3(H8 / (D8_WPB * D8_RPW)), dim3(256), 0, st, d_w, d_s, sd_q, sd_s,
-                     act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
+                      int I, int topk, const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st,
+                      int rows = 1) {
+  if (H != H8 || I != I8 || topk != TOPK8 || rows < 1 || rows > 64) return -1;
+  for (int r0 = 0; r0 < rows; r0 += 4) {
+    const int b = rows - r0 < 4 ? rows - r0 : 4;
+    const size_t xo = (size_t)r0 * H, ko = (size_t)r0 * topk, ao = (size_t)r0 * (topk + 1) * I;
+    auto go = [&](auto kb) {
+      constexpr int KB = decltype(kb)::value;
+      launch_decode_fp8_b<SF, SH, KB>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x + xo, idx + ko, wts + ko,
+                                      sgate + r0, res + xo, act + ao, y + xo, yb ? yb + xo : nullptr, nw, eps,
+                                      r0 + b == rows ? pf : nullptr, pf_bytes, st);
+    };
+    if (b == 1) go(std::integral_constant<int, 1>{});
+    else if (b == 2) go(std::integral_constant<int, 2>{});
+    else if (b == 3) go(std::integral_constant<int, 3>{});
+    else go(std::integral_constant<int, 4>{});
+  }
   return 0;
 }
 
@@ -223,4 +355,23 @@ API int dr_moe_decode_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, const
                                 const char* pf, size_t pf_bytes, hipStream_t st) {
   return launch_decode_fp8<1, Q8RowBF16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
                                          y, yb, H, I, topk, nw, eps, pf, pf_bytes, st);
+}
+
+API int dr_moe_decode_rows_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                               const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                               const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                               float* act, float* y, int rows, int H, int I, int topk, const float* nw, float eps,
+                               hipStream_t st) {
+  return launch_decode_fp8<0, Q8G128F16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
+                                         y, nullptr, H, I, topk, nw, eps, nullptr, 0, st, rows);
+}
+
+API int dr_moe_decode_rows_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, const uint8_t* d_w,
+                                     const uint16_t* d_s, const int8_t* sgu_q, const uint16_t* sgu_s,
+                                     const int8_t* sd_q, const uint16_t* sd_s, const float* x, const int* idx,
+                                     const float* wts, const float* sgate, const float* res, float* act, float* y,
+                                     uint16_t* yb, int rows, int H, int I, int topk, const float* nw, float eps,
+                                     hipStream_t st) {
+  return launch_decode_fp8<1, Q8RowBF16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
+                                         y, yb, H, I, topk, nw, eps, nullptr, 0, st, rows);
 }

@@ -12,6 +12,8 @@
 // int8 shared row.  Lane l owns chunk (l & 15) of experts (l >> 4) and 4 + (l >> 4) and 8
 // bytes of the shared row, so one row costs 2 x 16 + 8 bytes of loads per lane and the lane's
 // 72 activations stay in registers across rows.
+#include <type_traits>
+
 #include "common.hpp"
 
 using namespace drm;
@@ -63,7 +65,10 @@ struct SlotQ8H {
   DEV int operator()(int f) const { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
 };
 
-template <class SC, class SH>
+// B decode rows (B = 1: the engine's batch-1 call): routed blocks serve row blockIdx.y, the
+// shared-expert blocks of row 0 serve every row with one read of their weights.  Row r uses
+// x + r H, idx + r topk and act + r (topk + 1) I.
+template <class SC, class SH, int B>
 __global__ void __launch_bounds__(256)
     k_moe_gate_up_q4(const uint8_t* __restrict__ Q, const uint32_t* __restrict__ SM, const int8_t* __restrict__ shq,
                      const uint16_t* __restrict__ shs, const float* __restrict__ x, const int* __restrict__ idx,
@@ -72,6 +77,8 @@ __global__ void __launch_bounds__(256)
   __shared__ float4 xs[H / 4];
   const int lane = lane_id(), wave = wave_id();
   if (blockIdx.x < GU_NB_ROUTED) {
+    const int row = B > 1 ? (int)blockIdx.y : 0;
+    x += (size_t)row * H, idx += row * DEC_TOPK, act += (size_t)row * (DEC_TOPK + 1) * I;
     constexpr int BPE = GU_NB_ROUTED / DEC_TOPK;  // blocks per expert
     const int k = blockIdx.x / BPE, jb = blockIdx.x % BPE;
     const size_t e = (size_t)idx[k];
@@ -110,13 +117,16 @@ __global__ void __launch_bounds__(256)
     }
   } else {
     // shared expert, int8 [2I, H]: lane reads bytes [16 l, 16 l + 16) and [1024 + 16 l, ...)
+    if (B > 1 && blockIdx.y != 0) return;
     const int j = (blockIdx.x - GU_NB_ROUTED) * GU_WPB + wave;
     const int8_t* rg = shq + (size_t)j * H + lane * 16;
     const int8_t* ru = shq + (size_t)(I + j) * H + lane * 16;
     const uint4 g0 = ld16(rg), g1 = ld16(rg + 1024), u0 = ld16(ru), u1 = ld16(ru + 1024);
     const float sg0 = SH::scale(shs, j, lane * 16, H), sg1 = SH::scale(shs, j, 1024 + lane * 16, H);
     const float su0 = SH::scale(shs, I + j, lane * 16, H), su1 = SH::scale(shs, I + j, 1024 + lane * 16, H);
-    stage_xn<H>(x, nw, eps, xs, SlotQ8H{});
+    for (int row = 0; row < B; ++row) {
+    if (row) __syncthreads();  // every wave has read the previous row's inputs
+    stage_xn<H>(x + (size_t)row * H, nw, eps, xs, SlotQ8H{});
     float xa[16], xb[16], sa = 0.f, sb = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -136,99 +146,142 @@ __global__ void __launch_bounds__(256)
     }
     const float g = wave_sum(sg0 * (ga - 128.f * sa) + sg1 * (gb - 128.f * sb));
     const float u = wave_sum(su0 * (ua - 128.f * sa) + su1 * (ub - 128.f * sb));
-    if (lane == 0) act[DEC_TOPK * I + j] = silu(g) * u;
+    if (lane == 0) act[(size_t)row * (DEC_TOPK + 1) * I + DEC_TOPK * I + j] = silu(g) * u;
+    }
   }
 }
 
-template <class SC, class SH>
+// B decode rows: each wave owns output rows n0, n0 + 1 of every row r (routed rows of row r's
+// experts, one read of the shared rows for all B), the activations of all rows staged in LDS.
+template <class SC, class SH, int B>
 __global__ void __launch_bounds__(256)
     k_moe_down_q4(const uint8_t* __restrict__ Q, const uint32_t* __restrict__ SM, const int8_t* __restrict__ shq,
                   const uint16_t* __restrict__ shs, const float* __restrict__ act, const int* __restrict__ idx,
                   const float* __restrict__ wts, const float* __restrict__ sgate, const float* res, float* y,
                   uint16_t* yb, const char* pf, size_t pf_bytes) {
-  constexpr int H = DEC_H, I = DEC_I;
-  __shared__ float4 as[(DEC_TOPK + 1) * I / 4];
+  constexpr int H = DEC_H, I = DEC_I, AW = (DEC_TOPK + 1) * I / 4;  // act float4 per row
+  __shared__ float4 as[B * AW];
   const int lane = lane_id(), wave = wave_id();
   const int ka = lane >> 4, cc = lane & 15;
-  const size_t ea = (size_t)idx[ka], eb = (size_t)idx[4 + ka];
   const int n0 = (blockIdx.x * DN_WPB + wave) * DN_RPW;
-  uint4 qa[DN_RPW], qb[DN_RPW];
+  uint4 qa[B][DN_RPW], qb[B][DN_RPW];
+  uint32_t sa[B][DN_RPW], sb[B][DN_RPW];
   uint2 qs[DN_RPW];
-  uint32_t sa[DN_RPW], sb[DN_RPW];
   float ss[DN_RPW];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const size_t ea = (size_t)idx[b * DEC_TOPK + ka], eb = (size_t)idx[b * DEC_TOPK + 4 + ka];
+#pragma unroll
+    for (int r = 0; r < DN_RPW; ++r) {
+      const size_t n = (size_t)(n0 + r);
+      qa[b][r] = ld16(Q + (ea * H + n) * (I / 2) + cc * 16);
+      qb[b][r] = ld16(Q + (eb * H + n) * (I / 2) + cc * 16);
+      sa[b][r] = ld4(SM + (ea * H + n) * (I / 64) + (cc >> 1));
+      sb[b][r] = ld4(SM + (eb * H + n) * (I / 64) + (cc >> 1));
+    }
+  }
 #pragma unroll
   for (int r = 0; r < DN_RPW; ++r) {
     const size_t n = (size_t)(n0 + r);
-    qa[r] = ld16(Q + (ea * H + n) * (I / 2) + cc * 16);
-    qb[r] = ld16(Q + (eb * H + n) * (I / 2) + cc * 16);
-    sa[r] = SM[(ea * H + n) * (I / 64) + (cc >> 1)];
-    sb[r] = SM[(eb * H + n) * (I / 64) + (cc >> 1)];
     qs[r] = ld8(shq + n * I + lane * 8);
     ss[r] = SH::scale(shs, n, lane * 8, I);
   }
-  const float wa = wts[ka], wb = wts[4 + ka];
-  const float sgv = sigmoid(sgate[0]);
   // stage act: routed part as two 512-float4 halves with the 8-per-lane swizzle, shared part
   // (128 float4) with 2 per lane
-  const float4* a4 = reinterpret_cast<const float4*>(act);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = threadIdx.x + 256 * i;
-    as[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = a4[f];
-  }
-  if (threadIdx.x < 128) {
-    const int f = threadIdx.x;
-    as[1024 + (f & 1) * 64 + (f >> 1)] = a4[1024 + f];
+  for (int b = 0; b < B; ++b) {
+    const float4* a4 = reinterpret_cast<const float4*>(act + (size_t)b * (DEC_TOPK + 1) * I);
+    float4* ab = as + b * AW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      ab[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = a4[f];
+    }
+    if (threadIdx.x < 128) {
+      const int f = threadIdx.x;
+      ab[1024 + (f & 1) * 64 + (f >> 1)] = a4[1024 + f];
+    }
   }
   __syncthreads();
-  float xa[32], xb[32], xc[8];
-  float suma = 0.f, sumb = 0.f, sumc = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 v = as[i * 64 + lane], w = as[512 + i * 64 + lane];
-    xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
-    xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-    suma += (v.x + v.y) + (v.z + v.w);
-    sumb += (w.x + w.y) + (w.z + w.w);
-  }
+  for (int b = 0; b < B; ++b) {
+    const float4* ab = as + b * AW;
+    float xa[32], xb[32], xc[8];
+    float suma = 0.f, sumb = 0.f, sumc = 0.f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float4 v = as[1024 + i * 64 + lane];
-    xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
-    sumc += (v.x + v.y) + (v.z + v.w);
-  }
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = ab[i * 64 + lane], w = ab[512 + i * 64 + lane];
+      xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+      xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+      suma += (v.x + v.y) + (v.z + v.w);
+      sumb += (w.x + w.y) + (w.z + w.w);
+    }
 #pragma unroll
-  for (int r = 0; r < DN_RPW; ++r) {
-    float da = 0.f, db = 0.f;
-    da = dot8_q4(qa[r].x, xa + 0, da), db = dot8_q4(qb[r].x, xb + 0, db);
-    da = dot8_q4(qa[r].y, xa + 8, da), db = dot8_q4(qb[r].y, xb + 8, db);
-    da = dot8_q4(qa[r].z, xa + 16, da), db = dot8_q4(qb[r].z, xb + 16, db);
-    da = dot8_q4(qa[r].w, xa + 24, da), db = dot8_q4(qb[r].w, xb + 24, db);
-    float dc = dot4_u8b(qs[r].x, xc, 0.f);
-    dc = dot4_u8b(qs[r].y, xc + 4, dc);
-    const float2 pa = SC::pair(sa[r]), pb = SC::pair(sb[r]);
-    float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) + sgv * ss[r] * (dc - 128.f * sumc);
-    acc = wave_sum(acc);
-    const int n = n0 + r;
-    if (lane == 0) {
-      const float out = res[n] + acc;
-      y[n] = out;
-      if (yb) yb[n] = to_bf16(out);
+    for (int i = 0; i < 2; ++i) {
+      const float4 v = ab[1024 + i * 64 + lane];
+      xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
+      sumc += (v.x + v.y) + (v.z + v.w);
+    }
+    const float wa = wts[b * DEC_TOPK + ka], wb = wts[b * DEC_TOPK + 4 + ka];
+    const float sgv = sigmoid(sgate[b]);
+#pragma unroll
+    for (int r = 0; r < DN_RPW; ++r) {
+      float da = 0.f, db = 0.f;
+      da = dot8_q4(qa[b][r].x, xa + 0, da), db = dot8_q4(qb[b][r].x, xb + 0, db);
+      da = dot8_q4(qa[b][r].y, xa + 8, da), db = dot8_q4(qb[b][r].y, xb + 8, db);
+      da = dot8_q4(qa[b][r].z, xa + 16, da), db = dot8_q4(qb[b][r].z, xb + 16, db);
+      da = dot8_q4(qa[b][r].w, xa + 24, da), db = dot8_q4(qb[b][r].w, xb + 24, db);
+      float dc = dot4_u8b(qs[r].x, xc, 0.f);
+      dc = dot4_u8b(qs[r].y, xc + 4, dc);
+      const float2 pa = SC::pair(sa[b][r]), pb = SC::pair(sb[b][r]);
+      float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) + sgv * ss[r] * (dc - 128.f * sumc);
+      acc = wave_sum(acc);
+      const size_t n = (size_t)b * H + n0 + r;
+      if (lane == 0) {
+        const float out = res[n] + acc;
+        y[n] = out;
+        if (yb) yb[n] = to_bf16(out);
+      }
     }
   }
   warm_range(pf, pf_bytes);
 }
 
+template <class SC, class SH, int B>
+void launch_decode_b(const uint8_t* gu_q, const void* gu_sm, const uint8_t* d_q, const void* d_sm,
+                     const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                     const float* x, const int* idx, const float* wts, const float* sgate, const float* res, float* act,
+                     float* y, uint16_t* yb, const float* nw, float eps, const char* pf, size_t pf_bytes,
+                     hipStream_t st) {
+  hipLaunchKernelGGL((k_moe_gate_up_q4<SC, SH, B>), dim3(GU_NB_ROUTED + GU_NB_SHARED, B), dim3(256), 0, st, gu_q,
+                     (const uint32_t*)gu_sm, sgu_q, sgu_s, x, idx, act, nw, eps);
+  hipLaunchKernelGGL((k_moe_down_q4<SC, SH, B>), dim3(DEC_H / (DN_WPB * DN_RPW)), dim3(256), 0, st, d_q,
+                     (const uint32_t*)d_sm, sd_q, sd_s, act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
+}
+
+// rows independent decode rows (x, res, y: [rows, H]; idx, wts: [rows, topk]; act: rows x
+// (topk + 1) x I), launched 4 rows at a time
 template <class SC, class SH>
 int launch_decode(const uint8_t* gu_q, const void* gu_sm, const uint8_t* d_q, const void* d_sm, const int8_t* sgu_q,
                   const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s, const float* x, const int* idx,
                   const float* wts, const float* sgate, const float* res, float* act, float* y, uint16_t* yb, int H,
-                  int I, int topk, const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st) {
-  if (H != DEC_H || I != DEC_I || topk != DEC_TOPK) return -1;
-  hipLaunchKernelGGL((k_moe_gate_up_q4<SC, SH>), dim3(GU_NB_ROUTED + GU_NB_SHARED), dim3(256), 0, st, gu_q,
-                     (const uint32_t*)gu_sm, sgu_q, sgu_s, x, idx, act, nw, eps);
-  hipLaunchKernelGGL((k_moe_down_q4<SC, SH>), dim3(DEC_H / (DN_WPB * DN_RPW)), dim3(256), 0, st, d_q,
-                     (const uint32_t*)d_sm, sd_q, sd_s, act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
+                  int I, int topk, const float* nw, float eps, const char* pf, size_t pf_bytes, hipStream_t st,
+                  int rows = 1) {
+  if (H != DEC_H || I != DEC_I || topk != DEC_TOPK || rows < 1 || rows > 64) return -1;
+  for (int r0 = 0; r0 < rows; r0 += 4) {
+    const int b = rows - r0 < 4 ? rows - r0 : 4;
+    const size_t xo = (size_t)r0 * H, ko = (size_t)r0 * topk, ao = (size_t)r0 * (topk + 1) * I;
+    auto go = [&](auto kb) {
+      constexpr int KB = decltype(kb)::value;
+      launch_decode_b<SC, SH, KB>(gu_q, gu_sm, d_q, d_sm, sgu_q, sgu_s, sd_q, sd_s, x + xo, idx + ko, wts + ko,
+                                  sgate + r0, res + xo, act + ao, y + xo, yb ? yb + xo : nullptr, nw, eps,
+                                  r0 + b == rows ? pf : nullptr, pf_bytes, st);
+    };
+    if (b == 1) go(std::integral_constant<int, 1>{});
+    else if (b == 2) go(std::integral_constant<int, 2>{});
+    else if (b == 3) go(std::integral_constant<int, 3>{});
+    else go(std::integral_constant<int, 4>{});
+  }
   return 0;
 }
 
@@ -307,6 +360,24 @@ API int dr_moe_decode_bf16s(const uint8_t* gu_q, const uint16_t* gu_sm, const ui
                             const char* pf, size_t pf_bytes, hipStream_t st) {
   return launch_decode<ScaleBF16, Q8RowBF16>(gu_q, gu_sm, d_q, d_sm, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate,
                                              res, act, y, yb, H, I, topk, nw, eps, pf, pf_bytes, st);
+}
+
+API int dr_moe_decode_rows(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q, const uint16_t* d_sm,
+                           const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                           const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                           float* act, float* y, int rows, int H, int I, int topk, const float* nw, float eps,
+                           hipStream_t st) {
+  return launch_decode<ScaleF16, Q8G128F16>(gu_q, gu_sm, d_q, d_sm, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res,
+                                            act, y, nullptr, H, I, topk, nw, eps, nullptr, 0, st, rows);
+}
+
+API int dr_moe_decode_rows_bf16s(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q, const uint16_t* d_sm,
+                                 const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
+                                 const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                                 float* act, float* y, uint16_t* yb, int rows, int H, int I, int topk, const float* nw,
+                                 float eps, hipStream_t st) {
+  return launch_decode<ScaleBF16, Q8RowBF16>(gu_q, gu_sm, d_q, d_sm, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate,
+                                             res, act, y, yb, H, I, topk, nw, eps, nullptr, 0, st, rows);
 }
 
 API int dr_gemv_q4_bf16s(const uint8_t* q, const uint16_t* sm, const uint16_t* x, float* y, uint16_t* yb, int N, int K,

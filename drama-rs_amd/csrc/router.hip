@@ -111,6 +111,119 @@ __global__ void __launch_bounds__(RT_WPB * 64)
   }
 }
 
+// Decode router for B rows (B <= 8) in one launch: wave w of block b computes logit row
+// RT_WPB b + w for every row, its weight row loaded once.  The rows of x are staged in LDS,
+// wave r < B computes row r's canonical RMSNorm scale, and the block normalises the staged
+// rows in place (canon_norm4 is elementwise, so the values equal those k_router_topk forms in
+// registers).  Every logit has the canonical order of k_router_topk, so each row's logits,
+// picks and weights equal those of dr_router_topk on that row.  The last block loads the
+// logits of all rows at once and spreads the per-row work over its waves: for topk <= 8 the
+// 4 B group selections and B softmax denominators, then one rank merge per row; for topk > 8
+// one wave per row.  It resets the counter.
+template <int B>
+__global__ void __launch_bounds__(RT_WPB * 64)
+    k_router_topk_rows(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ nw,
+                       float eps, float* __restrict__ logits, int E, int topk, int* __restrict__ idx,
+                       float* __restrict__ wts, float* __restrict__ sgate, uint32_t* __restrict__ counter) {
+  constexpr int K = 2048, NCH = K / 8 / WAVE, NRM = K / 4 / WAVE, NT = RT_WPB * 64;
+  __shared__ float4 xs[B][K / 4];
+  __shared__ float s_inv[B];
+  __shared__ int s_last;
+  const int lane = lane_id(), wave = wave_id();
+  const int row = blockIdx.x * RT_WPB + wave;
+  uint4 w[NCH];
+  if (row <= E) {
+    const uint16_t* wr = W + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) w[j] = ld16(wr + (size_t)(lane + WAVE * j) * 8);
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* n4 = reinterpret_cast<const float4*>(nw);
+  float4 nv[K / 4 / NT];
+  if (nw) {
+#pragma unroll
+    for (int i = 0; i < K / 4 / NT; ++i) nv[i] = n4[threadIdx.x + NT * i];
+  }
+#pragma unroll
+  for (int i = threadIdx.x; i < B * K / 4; i += NT) xs[i / (K / 4)][i % (K / 4)] = x4[i];
+  __syncthreads();
+  if (nw) {
+    if (wave < B) {
+      float4 xr[NRM];
+#pragma unroll
+      for (int j = 0; j < NRM; ++j) xr[j] = xs[wave][lane + WAVE * j];
+      const float inv = canon_rms_inv_regs<NRM>(xr, eps);
+      if (lane == 0) s_inv[wave] = inv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < B; ++r)
+#pragma unroll
+      for (int i = 0; i < K / 4 / NT; ++i) {
+        const int c = threadIdx.x + NT * i;
+        xs[r][c] = canon_norm4(xs[r][c], s_inv[r], nv[i]);
+      }
+    __syncthreads();
+  }
+  if (row <= E) {
+#pragma unroll
+    for (int r = 0; r < B; ++r) {
+      float4 xa[NCH], xb[NCH];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + WAVE * j;
+        xa[j] = xs[r][2 * c], xb[j] = xs[r][2 * c + 1];
+      }
+      const float acc = canon_row_dot<NCH>(w, xa, xb);
+      if (lane == 0) __hip_atomic_store(logits + (size_t)r * (E + 1) + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __shared__ float lg[B][257];
+  __shared__ uint64_t s_cand[B][32];
+  __shared__ int s_sel[B][8];
+  __shared__ float s_mz[B][2];
+  for (int i = threadIdx.x; i < B * (E + 1); i += NT) {
+    const int r = i / (E + 1), e = i - r * (E + 1);
+    lg[r][e] = __hip_atomic_load(logits + (size_t)r * (E + 1) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (topk <= 8) {
+    for (int t = wave; t < 5 * B; t += RT_WPB) {
+      const int r = t / 5, sub = t - 5 * r;
+      if (sub < 4) {
+        int ck, ce;
+        canon_select_group8(lg[r], E, sub, &ck, &ce);
+        if (lane < 8) s_cand[r][sub * 8 + lane] = canon_cand64(ck, ce);
+      } else {
+        float m;
+        const float z = canon_softmax_z(lg[r], E, &m);
+        if (lane == 0) s_mz[r][0] = m, s_mz[r][1] = z;
+      }
+    }
+    __syncthreads();
+    for (int r = wave; r < B; r += RT_WPB) {
+      const int id = merge_picks(s_cand[r], s_sel[r], topk);
+      const float wt = canon_topk_weight(lg[r][lane < topk ? id : 0], s_mz[r][0], s_mz[r][1], topk);
+      if (lane < topk) idx[r * topk + lane] = id, wts[r * topk + lane] = wt;
+    }
+  } else {
+    for (int r = wave; r < B; r += RT_WPB) {
+      int my_idx;
+      float my_w;
+      canon_softmax_topk(lg[r], E, topk, &my_idx, &my_w);
+      if (lane < topk) idx[r * topk + lane] = my_idx, wts[r * topk + lane] = my_w;
+    }
+  }
+  if ((int)threadIdx.x < B) sgate[threadIdx.x] = lg[threadIdx.x][E];
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One row per block.  topk <= 8: waves 0..3 each pick the top 8 of 64 experts and wave 4
 // computes the softmax denominator, then wave 0 ranks the 32 candidates (the same selection
 // and weights as canon_softmax_topk, in less than half the time); topk > 8: wave 0 alone.
@@ -307,6 +420,20 @@ API int dr_router_topk(const uint16_t* W, const float* x, const float* nw, float
   if (K != 2048 || E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E) return -1;
   hipLaunchKernelGGL(k_router_topk<2048>, dim3((E + RT_WPB) / RT_WPB), dim3(RT_WPB * 64), 0, st, W, x, nw, eps, logits, E, topk,
                      idx, wts, sgate, counter);
+  return 0;
+}
+
+API int dr_router_topk_rows(const uint16_t* W, const float* x, const float* nw, float eps, float* logits, int E,
+                            int topk, int K, int rows, int* idx, float* wts, float* sgate, uint32_t* counter,
+                            hipStream_t st) {
+  if (K != 2048 || E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E || rows < 1 || rows > 8) return -1;
+  const dim3 g((E + RT_WPB) / RT_WPB), b(RT_WPB * 64);
+  switch (rows) {
+#define RT_ROWS(n) \
+  case n: hipLaunchKernelGGL(k_router_topk_rows<n>, g, b, 0, st, W, x, nw, eps, logits, E, topk, idx, wts, sgate, counter); break;
+    RT_ROWS(1) RT_ROWS(2) RT_ROWS(3) RT_ROWS(4) RT_ROWS(5) RT_ROWS(6) RT_ROWS(7) RT_ROWS(8)
+#undef RT_ROWS
+  }
   return 0;
 }
 

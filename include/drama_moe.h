@@ -210,6 +210,40 @@ int dr_moe_shared_prefill_bf16s(const int8_t* sgu_q, const dr_bf16* sgu_s, const
                                 const dr_bf16* sd_s, const dr_bf16* hn, int rows, dr_bf16* act, float* out, int h,
                                 int i, dr_stream_t st);
 
+/* Small decode batches (a few tokens decoded together, e.g. benchmark configuration 5's
+ * batch 4): the batch-1 chain dr_router_topk -> dr_moe_decode(_fp8) for `rows` independent
+ * rows in three launches instead of a prefill-style grouping.  Row r uses x + r k (f32),
+ * logits + r (e + 1), idx/wts + r topk, sgate + r; the experts of each row are streamed once
+ * per row and the shared expert once for up to four rows.  Routing of each row is bit-exact
+ * with dr_router_topk on that row.  No reference counterpart (the engine decodes one token
+ * per step).  dr_router_topk_rows: rows <= 8, counter as in dr_router_topk. */
+int dr_router_topk_rows(const dr_bf16* w, const float* x, const float* nw, float eps, float* logits, int e,
+                        int topk, int k, int rows, int* idx, float* wts, float* sgate, uint32_t* counter,
+                        dr_stream_t st);
+/* x, res, y [rows, h] (y may alias x and res), act scratch rows x (topk + 1) x i floats;
+ * 1 <= rows <= 64.  Same weights and formats as dr_moe_decode / dr_moe_decode_bf16s /
+ * dr_moe_decode_fp8 / dr_moe_decode_fp8_bf16s. */
+int dr_moe_decode_rows(const uint8_t* gu_q, const dr_half* gu_sm, const uint8_t* d_q, const dr_half* d_sm,
+                       const int8_t* sgu_q, const dr_half* sgu_s, const int8_t* sd_q, const dr_half* sd_s,
+                       const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                       float* act, float* y, int rows, int h, int i, int topk, const float* nw, float eps,
+                       dr_stream_t st);
+int dr_moe_decode_rows_bf16s(const uint8_t* gu_q, const dr_bf16* gu_sm, const uint8_t* d_q, const dr_bf16* d_sm,
+                             const int8_t* sgu_q, const dr_bf16* sgu_s, const int8_t* sd_q, const dr_bf16* sd_s,
+                             const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                             float* act, float* y, dr_bf16* yb, int rows, int h, int i, int topk, const float* nw,
+                             float eps, dr_stream_t st);
+int dr_moe_decode_rows_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                           const int8_t* sgu_q, const dr_half* sgu_s, const int8_t* sd_q, const dr_half* sd_s,
+                           const float* x, const int* idx, const float* wts, const float* sgate, const float* res,
+                           float* act, float* y, int rows, int h, int i, int topk, const float* nw, float eps,
+                           dr_stream_t st);
+int dr_moe_decode_rows_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, const uint8_t* d_w, const dr_bf16* d_s,
+                                 const int8_t* sgu_q, const dr_bf16* sgu_s, const int8_t* sd_q, const dr_bf16* sd_s,
+                                 const float* x, const int* idx, const float* wts, const float* sgate,
+                                 const float* res, float* act, float* y, dr_bf16* yb, int rows, int h, int i,
+                                 int topk, const float* nw, float eps, dr_stream_t st);
+
 /* Single int4 GEMV (benchmark configuration 1): y[n] = sum_k (q[n,k] scale + min) x[k] with
  * x bf16, bf16 (scale, min) pairs per 64-group, fp32 accumulation; y f32 and (nullable) yb
  * bf16.  Unsupported: k % 2048 != 0 or k > 8192 -> -1. */

@@ -198,7 +198,49 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
     cnt2 = pf.counts.cpu()
     skew = rec(ms2 * 1000, nbytes2, experts_hit=hit2, rows_per_expert_max=int(cnt2.max()),
                note="skewed: 10% of experts get 50% of the pairs; routing given, no router GEMM")
-    return {"uniform": uniform, "skewed": skew}
+    return {"uniform": uniform, "skewed": skew, "shared_expert": shared_prefill_compare(lib, st, pf.rows)}
+
+
+def shared_prefill_compare(lib, st, rows, iters=40, copies=8):
+    """The shared expert of a prefill layer two ways, on the reference's weight format (int8,
+    f16 scale per 128 inputs): the sequence the reference engine issues (src/engine.rs:351-355,
+    560-562: dr_dequant_q8 -> dr_gemm [rows x 1024 x 2048] -> dr_swiglu_rows -> dr_dequant_q8
+    -> dr_gemm [rows x 2048 x 512]) and the fused dr_moe_shared_prefill.  dr_gemm keeps the
+    router's canonical fp32 summation order (one symbol serves both), so it is not a fast GEMM."""
+    g = torch.Generator(device="cuda").manual_seed(61)
+    sp, P = st.cuda_stream, D.ptr
+    z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
+    Ws = []
+    for _ in range(copies):
+        Ws.append({"sgu_q": torch.randint(-127, 128, (2 * I, H), generator=g, device="cuda", dtype=torch.int8),
+                   "sgu_s": (torch.rand(2 * I, H // 128, generator=g, device="cuda") * 1e-3 + 1e-4).half(),
+                   "sd_q": torch.randint(-127, 128, (H, I), generator=g, device="cuda", dtype=torch.int8),
+                   "sd_s": (torch.rand(H, I // 128, generator=g, device="cuda") * 1e-3 + 1e-4).half()})
+    hn = bf16_bits(torch.randn(rows, H, generator=g, device="cuda"))
+    wbuf, hh, act, out = z(2 * I * H, torch.int16), z(rows * 2 * I), z(rows * I, torch.int16), z(rows * H)
+    h = ctypes.c_void_p()
+    lib.dr_cublas_create(ctypes.byref(h), sp)
+
+    def ref_seq(i):
+        w = Ws[i % copies]
+        lib.dr_dequant_q8(P(w["sgu_q"]), P(w["sgu_s"]), P(wbuf), 2 * I, H, sp)
+        lib.dr_gemm(h.value, P(hn), P(wbuf), P(hh), rows, 2 * I, H, 0.0)
+        lib.dr_swiglu_rows(P(hh), P(act), rows, I, sp)
+        lib.dr_dequant_q8(P(w["sd_q"]), P(w["sd_s"]), P(wbuf), H, I, sp)
+        lib.dr_gemm(h.value, P(act), P(wbuf), P(out), rows, H, I, 0.0)
+
+    def fused(i):
+        w = Ws[i % copies]
+        lib.dr_moe_shared_prefill(P(w["sgu_q"]), P(w["sgu_s"]), P(w["sd_q"]), P(w["sd_s"]), P(hn), rows, P(act), P(out),
+                                  H, I, sp)
+
+    ms_ref, ms_fused = timed(ref_seq, iters, st), timed(fused, iters, st)
+    wbytes = 2 * I * H + 2 * I * (H // 128) * 2 + H * I + H * (I // 128) * 2
+    nbytes = wbytes + rows * H * 2 + rows * H * 4
+    return {"reference_sequence": rec(ms_ref * 1000, nbytes, launches=5,
+                                      note="dr_dequant_q8 -> dr_gemm -> dr_swiglu_rows -> dr_dequant_q8 -> dr_gemm "
+                                           "(the reference engine's calls); bytes = int8 weights + scales + hn + out"),
+            "fused": rec(ms_fused * 1000, nbytes, launches=1, note="dr_moe_shared_prefill, same weights and rows")}
 
 
 def make_fp8_layer(seed):

@@ -61,7 +61,7 @@ static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
 static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT, "error codes");
 
 // Phase timestamps for development builds (-DST_TRACE): thread 0 of each block stores the
-// 100 MHz clock at points 0..7 and 11..14 of each layer (poll rounds at 8..10, 15) into
+// 100 MHz clock at points 0..7, 9 and 11..14 of each layer (poll rounds at 8, 10 and 15) into
 // words LL_WORDS.. of a larger ll buffer.
 #ifdef ST_TRACE
 #define ST_PUT(pt, v) \
@@ -227,7 +227,8 @@ struct SpecAct {
 template <class SC>
 struct StepQ4 {
   static constexpr bool kMinTerm = true;
-  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 285;  // first-poll offsets (measured)
+  // first-poll offsets (measured; kOffX: 195 -> 12.3, 225-235 -> 11.7-11.8, 285 -> 12.2 us/layer)
+  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 230;
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -311,7 +312,9 @@ struct StepQ4 {
 template <int SF>
 struct StepFP8 {
   static constexpr bool kMinTerm = false;
-  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 245;  // twice the gate_up bytes of int4 (measured)
+  // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
+  // 11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
+  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 175;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];
@@ -419,7 +422,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float s_asum[192];  // activation chunk sums (see SpecAct::post)
   __shared__ float s_xsum[64];   // int4: sums of the 32-input chunks of xn (lane l's chunk)
   __shared__ uint64_t s_cand[32];  // per-group top 8 (canon_cand64)
-  __shared__ float s_mz[2];
   __shared__ int s_abort;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   // A block that gives up (a bounded wait expired, or an earlier call did and sync was not
@@ -559,6 +561,11 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
     {
       const int my_idx = s_sel[wave][lane & (ST_TOPK - 1)];
+      // the next layer's record: a scalar load issued here returns while the gate_up loads
+      // are in flight (read at the activation barrier it would cost a round trip on the way
+      // to the residual publish; at the layer start its wait would hold up the router's LDS
+      // reads, which share the counter)
+      Ln = layers[l + 1 < L ? l + 1 : l];
       ST_MARK(3);
       const uint64_t t_topk = __builtin_amdgcn_s_memrealtime();
 
@@ -566,13 +573,14 @@ __global__ void __launch_bounds__(ST_NT, 1)
       const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
       typename F::GU gu;
       F::load_gu(Ly, ek, rj, lane, gu);
-      // the softmax denominator is needed only by the down phase: wave 4 computes it while
-      // its gate_up loads are in flight
+      // routing weights, needed only by the down phase: every wave computes the softmax
+      // denominator and its pick weights while its gate_up loads are in flight
       __builtin_amdgcn_sched_barrier(0);
-      if (wave == 4) {
+      float my_w;
+      {
         float m;
         const float z = canon_softmax_z(lg, E, &m);
-        if (lane == 0) s_mz[0] = m, s_mz[1] = z;
+        my_w = canon_topk_weight(lg[my_idx], m, z, ST_TOPK);
       }
 
       // ---- gate_up: two routed pairs per wave
@@ -619,9 +627,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
       // ---- next layer's known weights: issued after the activation poll (a wave's loads
       // return in order, so loads issued before a poll would delay it)
-      Ln = Ly;
       if (l + 1 < L) {
-        Ln = layers[l + 1];
         if (is_router) {
           const uint16_t* wr = Ln.router + (size_t)rrow * H;
 #pragma unroll
@@ -631,8 +637,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
         nwv = Ln.nw ? ldf4(Ln.nw + 4 * tid) : make_float4(1.f, 1.f, 1.f, 1.f);
       }
 
-      // ---- routing weights (s_mz is complete since the activation barrier)
-      const float my_w = canon_topk_weight(lg[my_idx], s_mz[0], s_mz[1], ST_TOPK);
+      ST_MARK(9);
       const float sgv = sigmoid(lg[E]);
       if (blockIdx.x == 0 && wave == 0) {
         if (idx_out && lane < ST_TOPK) idx_out[l * ST_TOPK + lane] = my_idx;
@@ -652,6 +657,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       dc = dot4_u8b(qs.y, xc + 4, dc);
       float acc = F::down(dn, as4, s_asum, my_w, lane) + sgv * SH::cvt(ssr) * (dc - 128.f * sumc);
       acc = wave_sum(acc);
+      ST_MARK(11);
       if (lane == 0) {
         const float y = res + acc;
         if (l + 1 < L) ll_put(ll + LL_X + n, y, tC);

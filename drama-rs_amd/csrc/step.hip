@@ -227,8 +227,8 @@ struct SpecAct {
 template <class SC>
 struct StepQ4 {
   static constexpr bool kMinTerm = true;
-  // first-poll offsets (measured; kOffX: 195 -> 12.3, 225-235 -> 11.7-11.8, 285 -> 12.2 us/layer)
-  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 230;
+  // first-poll offsets (measured; kOffX: 195 -> 12.3, 215-235 -> 11.6-11.8, 285 -> 12.2 us/layer)
+  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 215;
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -313,8 +313,8 @@ template <int SF>
 struct StepFP8 {
   static constexpr bool kMinTerm = false;
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
-  // 11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
-  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 175;
+  // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
+  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 165;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];
@@ -625,17 +625,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
       return;
     }
 
-      // ---- next layer's known weights: issued after the activation poll (a wave's loads
-      // return in order, so loads issued before a poll would delay it)
-      if (l + 1 < L) {
-        if (is_router) {
-          const uint16_t* wr = Ln.router + (size_t)rrow * H;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
-        }
-        if (is_shared) load_shared_pair<SH>(Ln, sj, lane, sp);
-        nwv = Ln.nw ? ldf4(Ln.nw + 4 * tid) : make_float4(1.f, 1.f, 1.f, 1.f);
-      }
 
       ST_MARK(9);
       const float sgv = sigmoid(lg[E]);
@@ -664,7 +653,19 @@ __global__ void __launch_bounds__(ST_NT, 1)
         else x[n] = y;
         if (xs_out) xs_out[(size_t)l * H + n] = y;
       }
-      nws[tid] = nwv;  // the next layer's norm weight (the router rows read nws before the logits barrier)
+      // ---- next layer's known weights: issued after the residual publish (issued before it,
+      // the compiler's wait for a spilled address ahead of the publish would wait for them
+      // too) and after the activation poll (a wave's loads return in order, so loads issued
+      // before a poll would delay it)
+      if (l + 1 < L) {
+        if (is_router) {
+          const uint16_t* wr = Ln.router + (size_t)rrow * H;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rw.w[j] = ld16(wr + (size_t)(lane + 64 * j) * 8);
+        }
+        if (is_shared) load_shared_pair<SH>(Ln, sj, lane, sp);
+        nwv = Ln.nw ? ldf4(Ln.nw + 4 * tid) : make_float4(1.f, 1.f, 1.f, 1.f);
+      }
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
@@ -672,6 +673,9 @@ __global__ void __launch_bounds__(ST_NT, 1)
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }
+      // the next layer's norm weight, stored after the poll (its load returns ahead of the
+      // poll's reads anyway); the router rows read nws after the barrier below
+      nws[tid] = nwv;
     }
     __syncthreads();
     ST_MARK(7);

@@ -286,7 +286,10 @@ int launch_decode(const uint8_t* gu_q, const void* gu_sm, const uint8_t* d_q, co
 }
 
 // ---- single int4 GEMV (configuration 1) ------------------------------------------------------
-constexpr int GV_WPB = 4, GV_RPW = 4;
+// One output row per wave, so a 1024-row GEMV spreads over 256 blocks (every CU).  The first
+// 2048-input segment of the row is requested before x is staged, so the weight fetch and the
+// x staging share one memory round trip.
+constexpr int GV_WPB = 4, GV_RPW = 1;
 
 template <class SC>
 __global__ void __launch_bounds__(256)
@@ -294,25 +297,29 @@ __global__ void __launch_bounds__(256)
               float* __restrict__ y, uint16_t* __restrict__ yb, int N, int K) {
   extern __shared__ float4 xsd[];
   const int lane = lane_id(), wave = wave_id();
-  // stage x (bf16) as fp32 float4 with the lane-major swizzle per 2048-element segment
-  for (int f = threadIdx.x; f < K / 4; f += blockDim.x) {
-    const uint2 v = ld8(x + (size_t)f * 4);
-    xsd[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
-  }
-  __syncthreads();
   const int row0 = (blockIdx.x * GV_WPB + wave) * GV_RPW;
-  float acc[GV_RPW];
-#pragma unroll
-  for (int r = 0; r < GV_RPW; ++r) acc[r] = 0.f;
-  for (int seg = 0; seg < K / 2048; ++seg) {
-    uint4 w[GV_RPW];
-    uint32_t s[GV_RPW];
+  uint4 w[GV_RPW];
+  uint32_t s[GV_RPW];
+  auto fetch = [&](int seg) {
 #pragma unroll
     for (int r = 0; r < GV_RPW; ++r) {
       const int row = row0 + r < N ? row0 + r : N - 1;
       w[r] = ld16(Q + (size_t)row * (K / 2) + seg * 1024 + lane * 16);
       s[r] = SM[(size_t)row * (K / 64) + seg * 32 + (lane >> 1)];
     }
+  };
+  fetch(0);
+  // stage x (bf16) as fp32 float4 with the lane-major swizzle per 2048-element segment
+  for (int f = threadIdx.x; f < K / 4; f += blockDim.x) {
+    const uint2 v = ld8(x + (size_t)f * 4);
+    xsd[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+  }
+  __syncthreads();
+  float acc[GV_RPW];
+#pragma unroll
+  for (int r = 0; r < GV_RPW; ++r) acc[r] = 0.f;
+  for (int seg = 0; seg < K / 2048; ++seg) {
+    if (seg) fetch(seg);
     float xv[32], xsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

@@ -259,4 +259,86 @@ DEV void warm_range(const char* pf, size_t bytes) {
   asm volatile("" ::"v"(acc));
 }
 
+// LDS slots of staged inputs, float4 f -> slot.  SlotQ4: lane l of a wave reads the 32 inputs
+// [32 l, 32 l + 32) of each 2048-input part as 8 float4 (slot i * 64 + l); SlotQ8H: lane l
+// reads the 16 inputs [16 l, 16 l + 16) of each 1024-input half as 4 float4.
+struct SlotQ4 {
+  DEV int operator()(int f) const { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
+};
+struct SlotQ8H {
+  DEV int operator()(int f) const { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
+};
+
+// Stage NR rows of RMSNorm(x) (nw == nullptr: x itself) in LDS, float4 f of a row at
+// Slot{}(f) (SlotQ4: the 32-element lane chunks of int4 rows; SlotQ8H: the 16-element lane
+// chunks of byte rows read as two 1024-byte halves).  load() issues the global loads unconditionally and ahead of everything issued after
+// it (loads return in order, so weight loads issued later do not delay the staging);
+// finish() reduces (partial sums added in wave order), normalises and writes LDS.  Every
+// thread of the block calls both.
+template <int H, int NT, int NR, class Slot>
+struct XStage {
+  static constexpr int NWV = NT / WAVE, PER = H / 4 / NT;
+  float4 v[NR][PER], w[PER];
+  DEV void load(const float* x, const float* nw) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* n4 = reinterpret_cast<const float4*>(nw ? nw : x);
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) v[r][i] = ldf4(x4 + r * (H / 4) + threadIdx.x + NT * i);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) w[i] = ldf4(n4 + threadIdx.x + NT * i);
+    issue_fence();
+  }
+  DEV void finish(bool norm, float eps, float4* xs) {
+    __shared__ float red[NR][NWV];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        ss += v[r][i].x * v[r][i].x + v[r][i].y * v[r][i].y + v[r][i].z * v[r][i].z + v[r][i].w * v[r][i].w;
+      ss = wave_sum(ss);
+      if (lane_id() == 0) red[r][wave_id()] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float t = red[r][0];
+#pragma unroll
+      for (int q = 1; q < NWV; ++q) t += red[r][q];
+      // without a norm weight: x * 1 * 1 == x exactly
+      const float inv = norm ? rsqrtf(t / (float)H + eps) : 1.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const float wx = norm ? w[i].x : 1.f, wy = norm ? w[i].y : 1.f, wz = norm ? w[i].z : 1.f,
+                    ww = norm ? w[i].w : 1.f;
+        v[r][i] = make_float4(v[r][i].x * inv * wx, v[r][i].y * inv * wy, v[r][i].z * inv * wz, v[r][i].w * inv * ww);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int f = threadIdx.x + NT * i;
+        xs[r * (H / 4) + Slot{}(f)] = v[r][i];
+      }
+    __syncthreads();
+  }
+};
+
+// Keeps weight registers opaque at this point, so the compiler cannot convert them to float
+// earlier (ahead of the input staging, or once outside a loop over rows): expanded to fp32,
+// every 16 bytes of weights would hold 16 registers.
+DEV void opaque(uint4& w) {
+  uint32_t a = w.x, b = w.y, c = w.z, d = w.w;
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  w = make_uint4(a, b, c, d);
+}
+template <int PPW>
+DEV void pin_weights(uint4 (&g0)[PPW], uint4 (&g1)[PPW], uint4 (&u0)[PPW], uint4 (&u1)[PPW]) {
+#pragma unroll
+  for (int p = 0; p < PPW; ++p) opaque(g0[p]), opaque(g1[p]), opaque(u0[p]), opaque(u1[p]);
+}
+
 }  // namespace drm

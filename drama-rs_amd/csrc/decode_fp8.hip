@@ -25,77 +25,6 @@ DEV float dot16_u8b(const uint4& w, const float* x, float acc) {
   return dot4_u8b(w.w, x + 12, acc);
 }
 
-// Stage NR rows of RMSNorm(x) (nw == nullptr: x itself) in LDS for the 16-element lane chunks
-// of the 2048-wide rows: float4 f of a row goes to lane (f & 255) >> 2 of part f >> 8, slot
-// f & 3.  load() issues the global loads unconditionally and ahead of everything issued after
-// it (loads return in order, so weight loads issued later do not delay the staging);
-// finish() reduces (partial sums added in wave order), normalises and writes LDS.  Every
-// thread of the block calls both.
-template <int H, int NT, int NR>
-struct XStage {
-  static constexpr int NWV = NT / WAVE, PER = H / 4 / NT;
-  float4 v[NR][PER], w[PER];
-  DEV void load(const float* x, const float* nw) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const float4* n4 = reinterpret_cast<const float4*>(nw ? nw : x);
-#pragma unroll
-    for (int r = 0; r < NR; ++r)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) v[r][i] = ldf4(x4 + r * (H / 4) + threadIdx.x + NT * i);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) w[i] = ldf4(n4 + threadIdx.x + NT * i);
-    issue_fence();
-  }
-  DEV void finish(bool norm, float eps, float4* xs) {
-    __shared__ float red[NR][NWV];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < PER; ++i)
-        ss += v[r][i].x * v[r][i].x + v[r][i].y * v[r][i].y + v[r][i].z * v[r][i].z + v[r][i].w * v[r][i].w;
-      ss = wave_sum(ss);
-      if (lane_id() == 0) red[r][wave_id()] = ss;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float t = red[r][0];
-#pragma unroll
-      for (int q = 1; q < NWV; ++q) t += red[r][q];
-      // without a norm weight: x * 1 * 1 == x exactly
-      const float inv = norm ? rsqrtf(t / (float)H + eps) : 1.f;
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const float wx = norm ? w[i].x : 1.f, wy = norm ? w[i].y : 1.f, wz = norm ? w[i].z : 1.f,
-                    ww = norm ? w[i].w : 1.f;
-        v[r][i] = make_float4(v[r][i].x * inv * wx, v[r][i].y * inv * wy, v[r][i].z * inv * wz, v[r][i].w * inv * ww);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int f = threadIdx.x + NT * i;
-        xs[r * (H / 4) + (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = v[r][i];
-      }
-    __syncthreads();
-  }
-};
-
-// Keeps the weight registers opaque until this point, so the compiler cannot convert them to
-// float ahead of the x staging (PPW pairs expanded to fp32 would need 64 PPW registers).
-DEV void opaque(uint4& w) {
-  uint32_t a = w.x, b = w.y, c = w.z, d = w.w;
-  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-  w = make_uint4(a, b, c, d);
-}
-template <int PPW>
-DEV void pin_weights(uint4 (&g0)[PPW], uint4 (&g1)[PPW], uint4 (&u0)[PPW], uint4 (&u1)[PPW]) {
-#pragma unroll
-  for (int p = 0; p < PPW; ++p) opaque(g0[p]), opaque(g1[p]), opaque(u0[p]), opaque(u1[p]);
-}
-
 DEV void unpack16(const float4* xs, int lane, float (&xa)[16], float (&xb)[16], float& sa, float& sb) {
   sa = 0.f, sb = 0.f;
 #pragma unroll
@@ -126,7 +55,7 @@ __global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(W
   __shared__ float4 xs[B * H / 4];
   if ((int)blockIdx.x >= NBS) {
     const int g = (blockIdx.x - NBS) * WPB + wave;
-    XStage<H, NT, B> xst;
+    XStage<H, NT, B, SlotQ8H> xst;
     xst.load(x, nw);
     uint4 g0[D], g1[D], u0[D], u1[D];
     uint32_t sr[D][4];
@@ -162,7 +91,7 @@ __global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(W
     }
   } else {
     const int j0 = (blockIdx.x * WPB + wave) * PPWS;
-    XStage<H, NT, B> xst;
+    XStage<H, NT, B, SlotQ8H> xst;
     xst.load(x, nw);
     uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
     float sg0[PPWS], sg1[PPWS], su0[PPWS], su1[PPWS];

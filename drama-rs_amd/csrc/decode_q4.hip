@@ -21,241 +21,232 @@ using namespace drm;
 namespace {
 
 constexpr int DEC_H = 2048, DEC_I = 512, DEC_TOPK = 8;
-constexpr int GU_WPB = 4, GU_PPW = 2;  // routed gate_up: waves per block, (gate, up) pairs per wave
-constexpr int GU_NB_ROUTED = DEC_TOPK * DEC_I / (GU_WPB * GU_PPW);
-constexpr int GU_NB_SHARED = DEC_I / GU_WPB;  // one shared pair per wave
-constexpr int DN_WPB = 4, DN_RPW = 2;         // down: waves per block, output rows per wave
 
-// Block-wide RMSNorm of x (H floats) into LDS, float4 f stored at slot(f).  Fast rsqrt: the
-// decode values are compared with a tolerance, only the router needs the canonical order.
-template <int H, class Slot>
-DEV void stage_xn(const float* __restrict__ x, const float* __restrict__ nw, float eps, float4* xs, Slot slot) {
-  __shared__ float red[4];
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  constexpr int PER = H / 4 / 256;
-  float4 v[PER], w[PER];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) v[i] = x4[threadIdx.x + 256 * i];
-  if (nw) {
-    const float4* n4 = reinterpret_cast<const float4*>(nw);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) w[i] = n4[threadIdx.x + 256 * i];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    ss = wave_sum(ss);
-    if (lane_id() == 0) red[wave_id()] = ss;
-    __syncthreads();
-    const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      v[i] = make_float4(v[i].x * inv * w[i].x, v[i].y * inv * w[i].y, v[i].z * inv * w[i].z, v[i].w * inv * w[i].w);
-  }
-#pragma unroll
-  for (int i = 0; i < PER; ++i) xs[slot(threadIdx.x + 256 * i)] = v[i];
-  __syncthreads();
-}
-
-// lane slices of 8 float4 (32 floats) per lane: f -> (f & 7) * 64 + (f >> 3) within 512-float4 parts
-struct SlotQ4 {
-  DEV int operator()(int f) const { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
-};
-// int8 K = 2048 rows read as bytes [16 l, 16 l + 16) and [1024 + 16 l, ...): 4 float4 per lane per half
-struct SlotQ8H {
-  DEV int operator()(int f) const { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
-};
-
-// B decode rows (B = 1: the engine's batch-1 call): routed blocks serve row blockIdx.y, the
-// shared-expert blocks of row 0 serve every row with one read of their weights.  Row r uses
-// x + r H, idx + r topk and act + r (topk + 1) I.
-template <class SC, class SH, int B>
-__global__ void __launch_bounds__(256)
+// gate_up of B decode rows.  Routed units are (row b, pick k, pair j), j fastest; the NBR
+// routed blocks' waves walk them spaced by the grid (wave g takes units g, g + NW, ..., so
+// waves running side by side read neighbouring rows of one expert), keeping D units in flight
+// and loading unit p + D once unit p is computed.  The shared-expert blocks, dispatched first
+// (PPWS pairs per wave, int8 rows read as two 1024-byte halves), serve all B rows with one read
+// of their weights.  x (and the norm weight) are requested before the weights, so the staging
+// overlaps the weight fetch (a wave's loads return in order).
+template <class SC, class SH, int WPB, int NBR, int D, int PPWS, int B>
+__global__ void __launch_bounds__(WPB * 64)
     k_moe_gate_up_q4(const uint8_t* __restrict__ Q, const uint32_t* __restrict__ SM, const int8_t* __restrict__ shq,
-                     const uint16_t* __restrict__ shs, const float* __restrict__ x, const int* __restrict__ idx,
-                     float* __restrict__ act, const float* __restrict__ nw, float eps) {
-  constexpr int H = DEC_H, I = DEC_I;
-  __shared__ float4 xs[H / 4];
+                     const uint16_t* __restrict__ shs, const float* x, const int* __restrict__ idx,
+                     float* __restrict__ act, const float* nw, float eps) {
+  constexpr int H = DEC_H, I = DEC_I, NT = WPB * 64, NW = NBR * WPB, PPW = B * DEC_TOPK * I / NW;
+  constexpr int NBS = I / (WPB * PPWS);
+  static_assert(PPW * NW == B * DEC_TOPK * I && D <= PPW, "units split evenly over the routed waves");
+  __shared__ float4 xs[B * H / 4];
   const int lane = lane_id(), wave = wave_id();
-  if (blockIdx.x < GU_NB_ROUTED) {
-    const int row = B > 1 ? (int)blockIdx.y : 0;
-    x += (size_t)row * H, idx += row * DEC_TOPK, act += (size_t)row * (DEC_TOPK + 1) * I;
-    constexpr int BPE = GU_NB_ROUTED / DEC_TOPK;  // blocks per expert
-    const int k = blockIdx.x / BPE, jb = blockIdx.x % BPE;
-    const size_t e = (size_t)idx[k];
-    const uint8_t* q = Q + e * (2 * I) * (H / 2) + lane * 16;
-    const uint32_t* sm = SM + e * (2 * I) * (H / 64) + (lane >> 1);
-    uint4 wg[GU_PPW], wu[GU_PPW];
-    uint32_t sg[GU_PPW], su[GU_PPW];
+  if ((int)blockIdx.x >= NBS) {
+    const int g = (blockIdx.x - NBS) * WPB + wave;
+    XStage<H, NT, B, SlotQ4> xst;
+    xst.load(x, nw);
+    uint4 wg[D], wu[D];
+    uint32_t sg[D], su[D];
+    auto issue = [&](int p, int d) {
+      const int u = g + NW * p, b = u / (DEC_TOPK * I), k = (u / I) % DEC_TOPK, j = u % I;
+      const size_t e = (size_t)idx[b * DEC_TOPK + k];
+      const uint8_t* q = Q + (e * (2 * I) + j) * (H / 2) + lane * 16;
+      const uint32_t* sm = SM + (e * (2 * I) + j) * (H / 64) + (lane >> 1);
+      wg[d] = ld16(q), wu[d] = ld16(q + (size_t)I * (H / 2));
+      sg[d] = ld4(sm), su[d] = ld4(sm + (size_t)I * (H / 64));
+      __builtin_amdgcn_sched_barrier(0);
+    };
 #pragma unroll
-    for (int p = 0; p < GU_PPW; ++p) {
-      const int j = (jb * GU_WPB + wave) * GU_PPW + p;
-      wg[p] = ld16(q + (size_t)j * (H / 2));
-      wu[p] = ld16(q + (size_t)(I + j) * (H / 2));
-      sg[p] = sm[(size_t)j * (H / 64)];
-      su[p] = sm[(size_t)(I + j) * (H / 64)];
-    }
-    stage_xn<H>(x, nw, eps, xs, SlotQ4{});
-    float xv[32], xsum = 0.f;
+    for (int p = 0; p < D; ++p) issue(p, p);
+    xst.finish(nw != nullptr, eps, xs);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = xs[i * 64 + lane];
-      xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
-      xsum += (v.x + v.y) + (v.z + v.w);
-    }
+    for (int p = 0; p < PPW; ++p) {
+      const int d = p % D;
+      const int u = g + NW * p, b = u / (DEC_TOPK * I), k = (u / I) % DEC_TOPK, j = u % I;
+      float xv[32], xsum = 0.f;
 #pragma unroll
-    for (int p = 0; p < GU_PPW; ++p) {
+      for (int i = 0; i < 8; ++i) {
+        const float4 v = xs[b * (H / 4) + i * 64 + lane];
+        xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
+        xsum += (v.x + v.y) + (v.z + v.w);
+      }
+      opaque(wg[d]), opaque(wu[d]);
       float qg = 0.f, qu = 0.f;
-      qg = dot8_q4(wg[p].x, xv + 0, qg), qu = dot8_q4(wu[p].x, xv + 0, qu);
-      qg = dot8_q4(wg[p].y, xv + 8, qg), qu = dot8_q4(wu[p].y, xv + 8, qu);
-      qg = dot8_q4(wg[p].z, xv + 16, qg), qu = dot8_q4(wu[p].z, xv + 16, qu);
-      qg = dot8_q4(wg[p].w, xv + 24, qg), qu = dot8_q4(wu[p].w, xv + 24, qu);
-      const float2 a = SC::pair(sg[p]), b = SC::pair(su[p]);
-      const float g = wave_sum(a.x * qg + a.y * xsum);
-      const float u = wave_sum(b.x * qu + b.y * xsum);
-      const int j = (jb * GU_WPB + wave) * GU_PPW + p;
-      if (lane == 0) act[k * I + j] = silu(g) * u;
+      qg = dot8_q4(wg[d].x, xv + 0, qg), qu = dot8_q4(wu[d].x, xv + 0, qu);
+      qg = dot8_q4(wg[d].y, xv + 8, qg), qu = dot8_q4(wu[d].y, xv + 8, qu);
+      qg = dot8_q4(wg[d].z, xv + 16, qg), qu = dot8_q4(wu[d].z, xv + 16, qu);
+      qg = dot8_q4(wg[d].w, xv + 24, qg), qu = dot8_q4(wu[d].w, xv + 24, qu);
+      const float2 pa = SC::pair(sg[d]), pb = SC::pair(su[d]);
+      if (p + D < PPW) issue(p + D, d);
+      const float gv = wave_sum(pa.x * qg + pa.y * xsum);
+      const float uv = wave_sum(pb.x * qu + pb.y * xsum);
+      if (lane == 0) act[(size_t)b * (DEC_TOPK + 1) * I + k * I + j] = silu(gv) * uv;
     }
   } else {
-    // shared expert, int8 [2I, H]: lane reads bytes [16 l, 16 l + 16) and [1024 + 16 l, ...)
-    if (B > 1 && blockIdx.y != 0) return;
-    const int j = (blockIdx.x - GU_NB_ROUTED) * GU_WPB + wave;
-    const int8_t* rg = shq + (size_t)j * H + lane * 16;
-    const int8_t* ru = shq + (size_t)(I + j) * H + lane * 16;
-    const uint4 g0 = ld16(rg), g1 = ld16(rg + 1024), u0 = ld16(ru), u1 = ld16(ru + 1024);
-    const float sg0 = SH::scale(shs, j, lane * 16, H), sg1 = SH::scale(shs, j, 1024 + lane * 16, H);
-    const float su0 = SH::scale(shs, I + j, lane * 16, H), su1 = SH::scale(shs, I + j, 1024 + lane * 16, H);
-    for (int row = 0; row < B; ++row) {
-    if (row) __syncthreads();  // every wave has read the previous row's inputs
-    stage_xn<H>(x + (size_t)row * H, nw, eps, xs, SlotQ8H{});
-    float xa[16], xb[16], sa = 0.f, sb = 0.f;
+    const int j0 = (blockIdx.x * WPB + wave) * PPWS;
+    XStage<H, NT, B, SlotQ8H> xst;
+    xst.load(x, nw);
+    uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
+    float sg0[PPWS], sg1[PPWS], su0[PPWS], su1[PPWS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 v = xs[i * 64 + lane], w = xs[256 + i * 64 + lane];
-      xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
-      xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-      sa += (v.x + v.y) + (v.z + v.w);
-      sb += (w.x + w.y) + (w.z + w.w);
+    for (int p = 0; p < PPWS; ++p) {
+      const int8_t* rg = shq + (size_t)(j0 + p) * H + lane * 16;
+      const int8_t* ru = shq + (size_t)(I + j0 + p) * H + lane * 16;
+      g0[p] = ld16(rg), g1[p] = ld16(rg + 1024), u0[p] = ld16(ru), u1[p] = ld16(ru + 1024);
     }
-    float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
-    const uint32_t gw0[4] = {g0.x, g0.y, g0.z, g0.w}, gw1[4] = {g1.x, g1.y, g1.z, g1.w};
-    const uint32_t uw0[4] = {u0.x, u0.y, u0.z, u0.w}, uw1[4] = {u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      ga = dot4_u8b(gw0[d], xa + 4 * d, ga), gb = dot4_u8b(gw1[d], xb + 4 * d, gb);
-      ua = dot4_u8b(uw0[d], xa + 4 * d, ua), ub = dot4_u8b(uw1[d], xb + 4 * d, ub);
+    for (int p = 0; p < PPWS; ++p) {
+      const int j = j0 + p;
+      sg0[p] = SH::scale(shs, j, lane * 16, H), sg1[p] = SH::scale(shs, j, 1024 + lane * 16, H);
+      su0[p] = SH::scale(shs, I + j, lane * 16, H), su1[p] = SH::scale(shs, I + j, 1024 + lane * 16, H);
     }
-    const float g = wave_sum(sg0 * (ga - 128.f * sa) + sg1 * (gb - 128.f * sb));
-    const float u = wave_sum(su0 * (ua - 128.f * sa) + su1 * (ub - 128.f * sb));
-    if (lane == 0) act[(size_t)row * (DEC_TOPK + 1) * I + DEC_TOPK * I + j] = silu(g) * u;
+    xst.finish(nw != nullptr, eps, xs);
+#pragma unroll 1
+    for (int r = 0; r < B; ++r) {
+      float xa[16], xb[16], sa = 0.f, sb = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 v = xs[r * (H / 4) + i * 64 + lane], w = xs[r * (H / 4) + 256 + i * 64 + lane];
+        xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+        xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+        sa += (v.x + v.y) + (v.z + v.w);
+        sb += (w.x + w.y) + (w.z + w.w);
+      }
+#pragma unroll
+      for (int p = 0; p < PPWS; ++p) {
+        // converted per row, not hoisted out of the row loop
+        opaque(g0[p]), opaque(g1[p]), opaque(u0[p]), opaque(u1[p]);
+        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
+        const uint32_t gw0[4] = {g0[p].x, g0[p].y, g0[p].z, g0[p].w}, gw1[4] = {g1[p].x, g1[p].y, g1[p].z, g1[p].w};
+        const uint32_t uw0[4] = {u0[p].x, u0[p].y, u0[p].z, u0[p].w}, uw1[4] = {u1[p].x, u1[p].y, u1[p].z, u1[p].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ga = dot4_u8b(gw0[q], xa + 4 * q, ga), gb = dot4_u8b(gw1[q], xb + 4 * q, gb);
+          ua = dot4_u8b(uw0[q], xa + 4 * q, ua), ub = dot4_u8b(uw1[q], xb + 4 * q, ub);
+        }
+        const float gv = wave_sum(sg0[p] * (ga - 128.f * sa) + sg1[p] * (gb - 128.f * sb));
+        const float uv = wave_sum(su0[p] * (ua - 128.f * sa) + su1[p] * (ub - 128.f * sb));
+        if (lane == 0) act[(size_t)r * (DEC_TOPK + 1) * I + DEC_TOPK * I + j0 + p] = silu(gv) * uv;
+      }
     }
   }
 }
 
-// B decode rows: each wave owns output rows n0, n0 + 1 of every row r (routed rows of row r's
-// experts, one read of the shared rows for all B), the activations of all rows staged in LDS.
-template <class SC, class SH, int B>
-__global__ void __launch_bounds__(256)
+// down of decode row blockIdx.y: wave w of block b owns output rows n0 .. n0 + RPW - 1; lane l
+// holds chunk (l & 15) of experts (l >> 4) and 4 + (l >> 4) and 8 bytes of the int8 shared row.
+// The row's activations are requested first and staged in LDS while the weights stream in.
+template <class SC, class SH, int WPB, int RPW>
+__global__ void __launch_bounds__(WPB * 64)
     k_moe_down_q4(const uint8_t* __restrict__ Q, const uint32_t* __restrict__ SM, const int8_t* __restrict__ shq,
-                  const uint16_t* __restrict__ shs, const float* __restrict__ act, const int* __restrict__ idx,
+                  const uint16_t* __restrict__ shs, const float* act, const int* __restrict__ idx,
                   const float* __restrict__ wts, const float* __restrict__ sgate, const float* res, float* y,
                   uint16_t* yb, const char* pf, size_t pf_bytes) {
-  constexpr int H = DEC_H, I = DEC_I, AW = (DEC_TOPK + 1) * I / 4;  // act float4 per row
-  __shared__ float4 as[B * AW];
+  constexpr int H = DEC_H, I = DEC_I, AW = (DEC_TOPK + 1) * I / 4, NT = WPB * 64, NA = 1024 / NT;
+  __shared__ float4 as[AW];
   const int lane = lane_id(), wave = wave_id();
-  const int ka = lane >> 4, cc = lane & 15;
-  const int n0 = (blockIdx.x * DN_WPB + wave) * DN_RPW;
-  uint4 qa[B][DN_RPW], qb[B][DN_RPW];
-  uint32_t sa[B][DN_RPW], sb[B][DN_RPW];
-  uint2 qs[DN_RPW];
-  float ss[DN_RPW];
+  const int ka = lane >> 4, cc = lane & 15, b = blockIdx.y;
+  const int n0 = (blockIdx.x * WPB + wave) * RPW;
+  act += (size_t)b * (DEC_TOPK + 1) * I, idx += b * DEC_TOPK, wts += b * DEC_TOPK;
+  // pick indices and weights with scalar loads, then the activations, then the weights
+  size_t ea, eb;
+  float wa, wb;
+  {
+    int ia[4], ib[4];
+    float fa[4], fb[4];
 #pragma unroll
-  for (int b = 0; b < B; ++b) {
-    const size_t ea = (size_t)idx[b * DEC_TOPK + ka], eb = (size_t)idx[b * DEC_TOPK + 4 + ka];
+    for (int i = 0; i < 4; ++i) ia[i] = idx[i], ib[i] = idx[4 + i], fa[i] = wts[i], fb[i] = wts[4 + i];
+    int sa_ = ia[0], sb_ = ib[0];
+    float ta = fa[0], tb = fb[0];
 #pragma unroll
-    for (int r = 0; r < DN_RPW; ++r) {
-      const size_t n = (size_t)(n0 + r);
-      qa[b][r] = ld16(Q + (ea * H + n) * (I / 2) + cc * 16);
-      qb[b][r] = ld16(Q + (eb * H + n) * (I / 2) + cc * 16);
-      sa[b][r] = ld4(SM + (ea * H + n) * (I / 64) + (cc >> 1));
-      sb[b][r] = ld4(SM + (eb * H + n) * (I / 64) + (cc >> 1));
+    for (int i = 1; i < 4; ++i) {
+      sa_ = ka == i ? ia[i] : sa_, sb_ = ka == i ? ib[i] : sb_;
+      ta = ka == i ? fa[i] : ta, tb = ka == i ? fb[i] : tb;
     }
+    ea = (size_t)sa_, eb = (size_t)sb_, wa = ta, wb = tb;
   }
+  const float sgv = sigmoid(sgate[b]);
+  const float4* a4 = reinterpret_cast<const float4*>(act);
+  float4 av[NA + 1];
 #pragma unroll
-  for (int r = 0; r < DN_RPW; ++r) {
+  for (int t = 0; t < NA; ++t) av[t] = ldf4(a4 + threadIdx.x + NT * t);
+  av[NA] = ldf4(a4 + 1024 + (threadIdx.x & 127));
+  issue_fence();
+  uint4 qa[RPW], qb[RPW];
+  uint32_t sa[RPW], sb[RPW], ssr[RPW];
+  uint2 qs[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
     const size_t n = (size_t)(n0 + r);
+    qa[r] = ld16(Q + (ea * H + n) * (I / 2) + cc * 16);
+    qb[r] = ld16(Q + (eb * H + n) * (I / 2) + cc * 16);
+    sa[r] = ld4(SM + (ea * H + n) * (I / 64) + (cc >> 1));
+    sb[r] = ld4(SM + (eb * H + n) * (I / 64) + (cc >> 1));
     qs[r] = ld8(shq + n * I + lane * 8);
-    ss[r] = SH::scale(shs, n, lane * 8, I);
+    ssr[r] = SH::raw(shs, n, lane * 8, I);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  // stage act: routed part as two 512-float4 halves with the 8-per-lane swizzle, shared part
-  // (128 float4) with 2 per lane
+  // routed part as two 512-float4 halves with the 8-per-lane swizzle, shared part (128 float4)
+  // with 2 per lane
 #pragma unroll
-  for (int b = 0; b < B; ++b) {
-    const float4* a4 = reinterpret_cast<const float4*>(act + (size_t)b * (DEC_TOPK + 1) * I);
-    float4* ab = as + b * AW;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = threadIdx.x + 256 * i;
-      ab[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = a4[f];
-    }
-    if (threadIdx.x < 128) {
-      const int f = threadIdx.x;
-      ab[1024 + (f & 1) * 64 + (f >> 1)] = a4[1024 + f];
-    }
+  for (int t = 0; t < NA; ++t) {
+    const int f = threadIdx.x + NT * t;
+    as[(f & ~511) + (f & 7) * 64 + ((f & 511) >> 3)] = av[t];
+  }
+  if ((int)threadIdx.x < 128) {
+    const int f = threadIdx.x;
+    as[1024 + (f & 1) * 64 + (f >> 1)] = av[NA];
   }
   __syncthreads();
+  float xa[32], xb[32], xc[8];
+  float suma = 0.f, sumb = 0.f, sumc = 0.f;
 #pragma unroll
-  for (int b = 0; b < B; ++b) {
-    const float4* ab = as + b * AW;
-    float xa[32], xb[32], xc[8];
-    float suma = 0.f, sumb = 0.f, sumc = 0.f;
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = as[i * 64 + lane], w = as[512 + i * 64 + lane];
+    xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
+    xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
+    suma += (v.x + v.y) + (v.z + v.w);
+    sumb += (w.x + w.y) + (w.z + w.w);
+  }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = ab[i * 64 + lane], w = ab[512 + i * 64 + lane];
-      xa[4 * i] = v.x, xa[4 * i + 1] = v.y, xa[4 * i + 2] = v.z, xa[4 * i + 3] = v.w;
-      xb[4 * i] = w.x, xb[4 * i + 1] = w.y, xb[4 * i + 2] = w.z, xb[4 * i + 3] = w.w;
-      suma += (v.x + v.y) + (v.z + v.w);
-      sumb += (w.x + w.y) + (w.z + w.w);
-    }
+  for (int i = 0; i < 2; ++i) {
+    const float4 v = as[1024 + i * 64 + lane];
+    xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
+    sumc += (v.x + v.y) + (v.z + v.w);
+  }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float4 v = ab[1024 + i * 64 + lane];
-      xc[4 * i] = v.x, xc[4 * i + 1] = v.y, xc[4 * i + 2] = v.z, xc[4 * i + 3] = v.w;
-      sumc += (v.x + v.y) + (v.z + v.w);
-    }
-    const float wa = wts[b * DEC_TOPK + ka], wb = wts[b * DEC_TOPK + 4 + ka];
-    const float sgv = sigmoid(sgate[b]);
-#pragma unroll
-    for (int r = 0; r < DN_RPW; ++r) {
-      float da = 0.f, db = 0.f;
-      da = dot8_q4(qa[b][r].x, xa + 0, da), db = dot8_q4(qb[b][r].x, xb + 0, db);
-      da = dot8_q4(qa[b][r].y, xa + 8, da), db = dot8_q4(qb[b][r].y, xb + 8, db);
-      da = dot8_q4(qa[b][r].z, xa + 16, da), db = dot8_q4(qb[b][r].z, xb + 16, db);
-      da = dot8_q4(qa[b][r].w, xa + 24, da), db = dot8_q4(qb[b][r].w, xb + 24, db);
-      float dc = dot4_u8b(qs[r].x, xc, 0.f);
-      dc = dot4_u8b(qs[r].y, xc + 4, dc);
-      const float2 pa = SC::pair(sa[b][r]), pb = SC::pair(sb[b][r]);
-      float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) + sgv * ss[r] * (dc - 128.f * sumc);
-      acc = wave_sum(acc);
-      const size_t n = (size_t)b * H + n0 + r;
-      if (lane == 0) {
-        const float out = res[n] + acc;
-        y[n] = out;
-        if (yb) yb[n] = to_bf16(out);
-      }
+  for (int r = 0; r < RPW; ++r) {
+    float da = 0.f, db = 0.f;
+    da = dot8_q4(qa[r].x, xa + 0, da), db = dot8_q4(qb[r].x, xb + 0, db);
+    da = dot8_q4(qa[r].y, xa + 8, da), db = dot8_q4(qb[r].y, xb + 8, db);
+    da = dot8_q4(qa[r].z, xa + 16, da), db = dot8_q4(qb[r].z, xb + 16, db);
+    da = dot8_q4(qa[r].w, xa + 24, da), db = dot8_q4(qb[r].w, xb + 24, db);
+    float dc = dot4_u8b(qs[r].x, xc, 0.f);
+    dc = dot4_u8b(qs[r].y, xc + 4, dc);
+    const float2 pa = SC::pair(sa[r]), pb = SC::pair(sb[r]);
+    float acc = wa * (pa.x * da + pa.y * suma) + wb * (pb.x * db + pb.y * sumb) +
+                sgv * SH::cvt(ssr[r]) * (dc - 128.f * sumc);
+    acc = wave_sum(acc);
+    const size_t n = (size_t)b * H + n0 + r;
+    if (lane == 0) {
+      const float out = res[n] + acc;
+      y[n] = out;
+      if (yb) yb[n] = to_bf16(out);
     }
   }
   warm_range(pf, pf_bytes);
 }
 
+// Launch shapes: batch 1 (the engine's per-layer chain) uses 256-thread blocks, many of them;
+// B > 1 uses 512-thread blocks, two per CU (as the FP8 kernels).
 template <class SC, class SH, int B>
 void launch_decode_b(const uint8_t* gu_q, const void* gu_sm, const uint8_t* d_q, const void* d_sm,
                      const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,
                      const float* x, const int* idx, const float* wts, const float* sgate, const float* res, float* act,
                      float* y, uint16_t* yb, const float* nw, float eps, const char* pf, size_t pf_bytes,
                      hipStream_t st) {
-  hipLaunchKernelGGL((k_moe_gate_up_q4<SC, SH, B>), dim3(GU_NB_ROUTED + GU_NB_SHARED, B), dim3(256), 0, st, gu_q,
+  constexpr int GW = B == 1 ? 4 : 8, GB = 512, GD = 2, GS = B == 1 ? 1 : 2, DW = B == 1 ? 4 : 8, DR = 2;
+  constexpr int NB = GB + DEC_I / (GW * GS);
+  hipLaunchKernelGGL((k_moe_gate_up_q4<SC, SH, GW, GB, GD, GS, B>), dim3(NB), dim3(GW * 64), 0, st, gu_q,
                      (const uint32_t*)gu_sm, sgu_q, sgu_s, x, idx, act, nw, eps);
-  hipLaunchKernelGGL((k_moe_down_q4<SC, SH, B>), dim3(DEC_H / (DN_WPB * DN_RPW)), dim3(256), 0, st, d_q,
+  hipLaunchKernelGGL((k_moe_down_q4<SC, SH, DW, DR>), dim3(DEC_H / (DW * DR), B), dim3(DW * 64), 0, st, d_q,
                      (const uint32_t*)d_sm, sd_q, sd_s, act, idx, wts, sgate, res, y, yb, pf, pf_bytes);
 }
 

@@ -188,9 +188,23 @@ __global__ void __launch_bounds__(RT_WPB * 64)
   __shared__ uint64_t s_cand[B][32];
   __shared__ int s_sel[B][8];
   __shared__ float s_mz[B][2];
-  for (int i = threadIdx.x; i < B * (E + 1); i += NT) {
-    const int r = i / (E + 1), e = i - r * (E + 1);
-    lg[r][e] = __hip_atomic_load(logits + (size_t)r * (E + 1) + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  {
+    // every row's logits requested at once (one round trip), then stored
+    constexpr int NL = (B * 257 + NT - 1) / NT;
+    float v[NL];
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = threadIdx.x + NT * t;
+      v[t] = i < B * (E + 1) ? __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = threadIdx.x + NT * t;
+      if (i < B * (E + 1)) {
+        const int r = i / (E + 1);
+        lg[r][i - r * (E + 1)] = v[t];
+      }
+    }
   }
   __syncthreads();
   if (topk <= 8) {

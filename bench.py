@@ -41,6 +41,9 @@ def parse():
                     help="only configuration 4 (prefill, 8 resident layers): the run profiled for the grouped GEMM")
     ap.add_argument("--profile-fp8", action="store_true",
                     help="only configuration 5 (FP8 decode, batch 1 and 4, int8 lm_head): the run profiled for its kernels")
+    ap.add_argument("--profile-small", action="store_true",
+                    help="only configurations 1 (one int4 GEMV) and 2 (one decode layer per launch, fused and "
+                         "chained) over --layers resident layers: the run profiled for their kernels")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only a 1 GiB device-to-device copy, 5 times: calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
@@ -221,6 +224,28 @@ def main():
         for L in layers:
             record_layer(L)
 
+    def config2_single_layer(iters=200):
+        # one decode layer per call (the fused step over one layer, and the per-layer chain),
+        # rotating over the resident layers so that no call finds its weights in the MALL
+        import benchcfg
+
+        def fused_one(i):
+            rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * (i % nl), 1, P(x), E, H, I, TOPK, 1e-6, P(ll),
+                                              P(sync), None, None, None, None, sp)
+            assert rc == 0
+        out = {}
+        for key, fn in (("fused_one_layer", fused_one), ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
+            ms = benchcfg.timed(fn, iters, st)
+            out[key] = benchcfg.rec(ms * 1000, bytes_step // nl)
+        out["note"] = "one launch (fused) or three launches (chain) per layer, launch latency included"
+        return out
+
+    if args.profile_small:
+        import benchcfg
+
+        print(json.dumps({"cfg2_one_layer": config2_single_layer(), "cfg1_gemv_int4": benchcfg.config1_gemv(lib, st)}))
+        return
+
     # ---- parity spot check: layer 0 of the first step against the CPU oracle
     parity = None
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -337,21 +362,6 @@ def main():
         import benchcfg
 
         extra = {}
-
-        def config2_single_layer(iters=200):
-            # one decode layer per call (the fused step over one layer, and the per-layer chain),
-            # rotating over the resident layers so that no call finds its weights in the MALL
-            def fused_one(i):
-                rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * (i % nl), 1, P(x), E, H, I, TOPK, 1e-6, P(ll),
-                                                  P(sync), None, None, None, None, sp)
-                assert rc == 0
-            out = {}
-            for key, fn in (("fused_one_layer", fused_one), ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
-                ms = benchcfg.timed(fn, iters, st)
-                out[key] = benchcfg.rec(ms * 1000, bytes_step // nl)
-            out["note"] = "one launch (fused) or three launches (chain) per layer, launch latency included"
-            return out
-
         for name, fn in (("cfg2_one_layer", config2_single_layer),
                          ("cfg1_gemv_int4", lambda: benchcfg.config1_gemv(lib, st)),
                          ("cfg4_prefill_int4", lambda: (benchcfg.config4_prefill(lib, layers, st, iters=10),  # warm-up

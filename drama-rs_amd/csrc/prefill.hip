@@ -379,13 +379,6 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   // conversion would cost two instructions per dword instead of one
   uint32_t q_mask = 0x000f000fu, q_bias = 0x43004300u;
   asm volatile("" : "+v"(q_mask), "+v"(q_bias));
-  // zero tokens for the int4 pair MFMAs (K / 8 blocks: every offset a pair's read adds stays
-  // inside); each wave writes the whole block itself before its own reads, so no barrier
-  const uint4* zeros = reinterpret_cast<const uint4*>(ups + (MODE == 0 ? 2 * PF_GRPW * WR * 64 : 0));
-  if (F::paired) {
-    uint4* z = const_cast<uint4*>(zeros);
-    for (int i = lane; i < K / 8; i += 64) z[i] = make_uint4(0, 0, 0, 0);
-  }
 
   Item cur = item_at(blockIdx.x);
   if (!cur.valid) return;
@@ -436,16 +429,8 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     if (MODE == 0 && !up && pend.valid) finish_gate(pend, k - 1);  // (at mid-item: measured slower)
     const uint4* xb = xs + (k & 1) * BUF;
     const uint4* xrow = xb + (size_t)c16 * (K / 8);
-    // int4 pairs: lanes g = 0, 1 carry the first group of a pair, g = 2, 3 the second; for the
-    // MFMA of one group the other lanes read the zero block instead of their tokens
-    const uint4* xa_base[4];
-    const uint4* xb_base[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4* own = xrow + ((4 * g + j) ^ c16);
-      xa_base[j] = g < 2 ? own : zeros;
-      xb_base[j] = g < 2 ? zeros : own;
-    }
+    // int4 pairs: first 8-input token block of this lane's swapped words (see compute)
+    const int tb = 4 * (g & 1) + 2 * (g >> 1);
     f32x4 tA = {0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const Step<F>& sa, int G0) {
       if constexpr (F::paired) {
@@ -467,15 +452,19 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
           const int P = G0 / 2 + pp;
-          const uint32_t wd[4] = {sa.raw[pp].x, sa.raw[pp].y, sa.raw[pp].z, sa.raw[pp].w};
-          f32x4 ua = {0.f, 0.f, 0.f, 0.f}, ub = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // one MFMA per group of the pair: the lanes of the other group read zero tokens
-            const uint4 f = q4_frag(wd[j], q_mask, q_bias);
-            ua = mfma(xa_base[j][P * 16], f, ua);
-            ub = mfma(xb_base[j][P * 16], f, ub);
-          }
+          // Lane (c16, g) holds nibbles [32 g, 32 g + 32) of the pair's 128 (g < 2: group A,
+          // g >= 2: group B), word j its inputs + 8 j.  Swapping words 2, 3 of lanes 0..31 with
+          // words 0, 1 of lanes 32..63 (same weight row c16) leaves every lane with two words of
+          // each group: fa0 / fa1 hold group A inputs 8 tb .. 8 tb + 15 and fb0 / fb1 the same of
+          // group B (tb = 4 (g & 1) + 2 (g >> 1), in 8-input blocks), so each group takes two
+          // full MFMAs against token blocks tb, tb + 1 (A) and tb + 8, tb + 9 (B).
+          const auto s02 = __builtin_amdgcn_permlane32_swap(sa.raw[pp].x, sa.raw[pp].z, false, false);
+          const auto s13 = __builtin_amdgcn_permlane32_swap(sa.raw[pp].y, sa.raw[pp].w, false, false);
+          const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+          const f32x4 ua = mfma(xrow[(16 * P + tb + 1) ^ c16], q4_frag(s13[0], q_mask, q_bias),
+                                mfma(xrow[(16 * P + tb) ^ c16], q4_frag(s02[0], q_mask, q_bias), z4));
+          const f32x4 ub = mfma(xrow[(16 * P + tb + 9) ^ c16], q4_frag(s13[1], q_mask, q_bias),
+                                mfma(xrow[(16 * P + tb + 8) ^ c16], q4_frag(s02[1], q_mask, q_bias), z4));
           const uint32_t sw[4] = {sa.sc.x, sa.sc.y, sa.sc.z, sa.sc.w};
           const float sca = F::scale_val(sw[2 * pp]).x, scb = F::scale_val(sw[2 * pp + 1]).x;
 #pragma unroll
@@ -882,7 +871,7 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
   // grouped experts: a persistent grid of as many blocks as are resident at once, walking the
   // work items (expert, token pass, row block) the kernel derives from counts
   const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
-                     (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0) + (F::paired ? (size_t)K * 2 : 0);
+                     (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0);
   auto kern = mode == 0 ? k_grouped<F, 0, 2048> : k_grouped<F, 1, 512>;
   int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E,

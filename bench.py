@@ -335,10 +335,10 @@ def main():
     lib.dr_graph_destroy(fexec)
     fused_ok = int(sync[1].item()) == 0
 
-    # ---- the same step with the routed activations exchanged as 24-bit floats (opt-in mode)
-    fused_a24_ms = float("nan")
+    # ---- the same step with every routed activation exchanged as a full fp32 plus a 32-bit tag
+    fused_a32_ms = float("nan")
     if not args.profile:
-        lib.dr_step_set_act_exchange(24)
+        lib.dr_step_set_act_exchange(32)
         for _ in range(args.warmup):
             fused_step()
         torch.cuda.synchronize()
@@ -347,8 +347,8 @@ def main():
             fused_step()
         fe1.record(st)
         torch.cuda.synchronize()
-        fused_a24_ms = fe0.elapsed_time(fe1) / args.steps
-        lib.dr_step_set_act_exchange(32)
+        fused_a32_ms = fe0.elapsed_time(fe1) / args.steps
+        lib.dr_step_set_act_exchange(0)
 
     # ---- per-layer kernel chain (router, gate_up, down per layer): eager and graph timing
     eager_ms = graph_ms = float("nan")
@@ -427,16 +427,17 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights, fp32 accumulate, fp32 activations between workgroups",
+        "dtype": "int4 weights, fp32 accumulate; routed activations exchanged between workgroups as fp32 "
+                 "rounded to 21 mantissa bits (the 2 low bits carry the exchange phase, relative error <= 2^-22)",
         "data": "synthetic (seeded torch RNG on device, shapes of BASELINE config 3)",
         "config": {"workload": "cfg3: 40-layer int4 routed-expert decode step, batch 1, top-8 of 256, hidden 2048, "
                                "expert intermediate 512, int8 shared expert; one fused persistent launch per step "
                                "(dr_moe_decode_step_bf16s)",
                    "layers": nl, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I},
         "fused_graph_ms_per_step": round(fused_graph_ms, 4),
-        "fused_act24_us_per_layer": None if args.profile else round(fused_a24_ms * 1000.0 / nl, 3),
-        "fused_act24_note": "the same step with the routed activations exchanged as 24-bit floats "
-                            "(dr_step_set_act_exchange(24), relative error <= 2^-16)",
+        "fused_act32_us_per_layer": None if args.profile else round(fused_a32_ms * 1000.0 / nl, 3),
+        "fused_act32_note": "the same step with every routed activation exchanged as a full fp32 with a 32-bit "
+                            "phase tag (dr_step_set_act_exchange(32)), as the reference's fp32 act buffer",
         "engine_one_layer_us": (extra or {}).get("cfg2_one_layer", {}).get("fused_one_layer", {}).get("us"),
         "engine_one_layer_note": "one MoE layer per launch (the engine interleaves attention between MoE "
                                  "layers, so a drop-in caller launches the step with n_layers = 1)",

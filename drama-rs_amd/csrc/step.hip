@@ -55,7 +55,8 @@ constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrea
 
 // slot arrays (64-bit words) inside the caller's ll buffer
 // The activation region holds the 4096 routed activations either one fp32 per word (A32) or
-// two 24-bit floats per word, then the 512 shared ones (one fp32 per word).
+// two fp32 per word with the phase in their two low mantissa bits, then the 512 shared ones
+// (one fp32 per word).
 constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + ST_TOPK * ST_I + ST_I, LL_WORDS = LL_X + ST_H;
 static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
 static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT, "error codes");
@@ -82,20 +83,23 @@ DEV uint64_t ll_get(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Two activations in one word: tag (16 bits) and both values rounded to nearest-even
-// 24-bit floats (sign, exponent, 15 mantissa bits; relative error <= 2^-16).  The 16-bit
-// tag still tells the current phase from the slot's previous content: that always carries
-// the previous layer's tag (3 less) or the previous launch's (a different epoch).
-DEV uint32_t f24(float v) {
+// Two activations in one word, each an fp32 whose two low mantissa bits carry the phase t2:
+// the value rounded to 21 mantissa bits (relative error <= 2^-22; infinities and NaNs are
+// not rounded, and an infinity comes out as a NaN), then t2 in bits 0-1.  Every 32-bit half
+// carries its own phase, so the word needs no single-copy atomicity beyond 32 bits.  t2 is
+// the running count of layers of all launches on this ll / sync pair plus one, mod 4
+// (sync[2] holds the count): a slot always holds the previous layer's value, whose t2 differs
+// by one, or zero (t2 0) before the first call.
+DEV uint32_t enc_t2(float v, uint32_t t2) {
   const uint32_t u = __float_as_uint(v);
-  return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+  return (((u & 0x7f800000u) == 0x7f800000u ? u : u + 2u) & ~3u) | t2;
 }
-DEV void ll_put2(uint64_t* p, float a, float b, uint32_t tag) {
-  const uint64_t w = ((uint64_t)(tag & 0xffffu) << 48) | ((uint64_t)f24(a) << 24) | (uint64_t)f24(b);
+DEV void ll_put2(uint64_t* p, float a, float b, uint32_t t2) {
+  const uint64_t w = ((uint64_t)enc_t2(b, t2) << 32) | (uint64_t)enc_t2(a, t2);
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 DEV float2 ll_val2(uint64_t w) {
-  return make_float2(__uint_as_float((uint32_t)(w >> 16) & 0xffffff00u), __uint_as_float((uint32_t)(w << 8)));
+  return make_float2(__uint_as_float((uint32_t)w & ~3u), __uint_as_float((uint32_t)(w >> 32) & ~3u));
 }
 
 DEV void wait_until(uint64_t t) {
@@ -161,20 +165,21 @@ struct Spec32 {
 
 // activations, routed then shared, stored into the down slots of the weight format F.
 // A32: words 0..4095 hold routed element w (fp32, 32-bit tag), rows i < 64; otherwise words
-// 0..2047 hold routed elements 2w, 2w + 1 as 24-bit floats (16-bit tag), rows i < 32.  The
-// 512 shared elements follow, one fp32 per word, in the last 8 rows.
+// 0..2047 hold routed elements 2w (low half) and 2w + 1 (high half) with the in-band phase t2,
+// rows i < 32.  The 512 shared elements follow, one fp32 per word (32-bit tag), in the last 8
+// rows.
 template <class F, bool A32>
 struct SpecAct {
   static constexpr int kRouted = A32 ? 64 : 32, kRows = kRouted + 8, kSharedWord = kRouted * 64;
-  uint32_t tag;
+  uint32_t tag, t2;
   float* dst;   // as4 as floats
   float* sums;  // [0, 128): sums of the 32-element routed chunks (int4), [128, 192): of the 8-element shared chunks
   DEV bool valid(int r, int) const { return r < kRows; }
   DEV uint64_t ready(int i) const {
-    return !A32 && i < kRouted ? (uint64_t)(tag & 0xffffu) << 48 : (uint64_t)tag << 32;
+    return !A32 && i < kRouted ? ((uint64_t)t2 << 32) | t2 : (uint64_t)tag << 32;
   }
   DEV bool ok(int i, uint64_t v) const {
-    return !A32 && i < kRouted ? (v >> 48) == (tag & 0xffffu) : (uint32_t)(v >> 32) == tag;
+    return !A32 && i < kRouted ? (v & 0x300000003ull) == (((uint64_t)t2 << 32) | t2) : (uint32_t)(v >> 32) == tag;
   }
   DEV void store(int i, int w, uint64_t v) const {
     if (i < kRouted) {
@@ -229,6 +234,9 @@ struct StepQ4 {
   static constexpr bool kMinTerm = true;
   // first-poll offsets (measured; kOffX: 195 -> 12.3, 215-235 -> 11.6-11.8, 285 -> 12.2 us/layer)
   static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 215;
+  // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
+  // 400 -> 11.5 us/layer)
+  static constexpr uint32_t kOffActIb = 375;
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -315,6 +323,8 @@ struct StepFP8 {
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
   static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 165;
+  // in-band activation phase: 400 -> 12.6, 430 -> 11.8, 460-470 -> 11.7, 510 -> 12.0 us/layer
+  static constexpr uint32_t kOffActIb = 465;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];
@@ -441,6 +451,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   const int g = blockIdx.x * ST_WPB + wave;
   const uint32_t epoch = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tag0 = epoch * ST_TAG_STRIDE + 1;
+  const uint32_t lbase = __hip_atomic_load(sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   const bool is_router = (wave == 0 && (int)blockIdx.x <= E) || (wave == 1 && blockIdx.x == 0 && E == ST_MAXE);
   const int rrow = wave == 0 ? (int)blockIdx.x : ST_MAXE;
@@ -474,7 +485,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
   dr_decode_layer Ln = Ly;
   for (int l = 0; l < L; ++l) {
-    const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2;
+    const uint32_t tA = tag0 + 3 * l, tB = tA + 1, tC = tA + 2, t2 = (lbase + l + 1) & 3u;
     ST_MARK(0);
     const uint64_t t_layer = __builtin_amdgcn_s_memrealtime();
     float res;  // x[n], read now: the poller overwrites xr4 during the down phase
@@ -592,7 +603,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
             ll_put(ll + LL_ACT + rk * I + rj, av[0], tB);
             ll_put(ll + LL_ACT + rk * I + rj + 1, av[1], tB);
           } else {
-            ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], tB);
+            ll_put2(ll + LL_ACT + ((rk * I + rj) >> 1), av[0], av[1], t2);
           }
         }
       }
@@ -610,7 +621,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       if (poller) {
         ST_MARKW(12, 7);
         const uint32_t r = poll_wave<SpecAct<F, A32>::kRows / ST_NP, ST_NP>(
-            ll + LL_ACT, pw, SpecAct<F, A32>{tB, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + F::kOffAct, tmo);
+            ll + LL_ACT, pw, SpecAct<F, A32>{tB, t2, reinterpret_cast<float*>(as4), s_asum}, sync, t_topk + (A32 ? F::kOffAct : F::kOffActIb), tmo);
         if (!r && lane == 0) s_abort = 1;
         ST_MARKW(13, 7);
 #ifdef ST_TRACE
@@ -685,7 +696,10 @@ __global__ void __launch_bounds__(ST_NT, 1)
     }
     Ly = Ln;
   }
-  if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (blockIdx.x == 0 && tid == 0) {
+    __hip_atomic_store(sync + 2, lbase + (uint32_t)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // The grid needs all ST_NB workgroups resident at once; checked once per device.
@@ -704,9 +718,10 @@ int step_grid_ok(const void* kernel) {
 
 std::atomic<uint64_t> g_wait_ticks{ST_TIMEOUT_TICKS};
 
-// Transport of the routed activations: fp32 (default) or 24-bit floats (half the words);
+// Transport of the routed activations: two fp32 per word with the phase in their two low
+// mantissa bits (default: half the words of the other form) or fp32 with a 32-bit tag per word;
 // dr_step_set_act_exchange selects it for later launches.
-std::atomic<int> g_act_bits{32};
+std::atomic<int> g_act_bits{30};
 
 template <class F, class SH, bool A32>
 int launch_step_as(const dr_decode_layer* layers, int L, float* x, int E, float eps, uint64_t* ll, uint32_t* sync,
@@ -726,7 +741,7 @@ int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, in
                 hipStream_t st) {
   if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || L < 1 || L > ST_MAXL) return -1;
   if (!layers || !x || !ll || !sync) return -1;
-  if (g_act_bits.load(std::memory_order_relaxed) == 24)
+  if (g_act_bits.load(std::memory_order_relaxed) == 30)
     return launch_step_as<F, SH, false>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
   return launch_step_as<F, SH, true>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
 }
@@ -784,8 +799,8 @@ API int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_la
 }
 
 API int dr_step_set_act_exchange(int bits) {
-  if (bits != 32 && bits != 24) return -1;
-  g_act_bits.store(bits, std::memory_order_relaxed);
+  if (bits != 0 && bits != 32 && bits != 30) return -1;
+  g_act_bits.store(bits ? bits : 30, std::memory_order_relaxed);
   return 0;
 }
 

@@ -303,10 +303,13 @@ int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, in
 int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                              int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
                              float* sgate_out, float* xs_out, dr_stream_t st);
-/* Transport of the routed activations between the fused step's workgroups, for later launches:
- * 32 (default) carries them as fp32, like the reference's act buffer (kernels/drama.cu:493,516);
- * 24 packs two 24-bit floats (15-bit mantissa, relative error <= 2^-16) per slot, half the
- * exchange traffic.  Other values -> -1. */
+/* Transport of the routed activations between the fused step's workgroups, for later launches.
+ * 30 (default; 0 restores it) packs two fp32 per slot with the exchange phase in the two low
+ * mantissa bits of each: the activations reach the down projection rounded to 21 mantissa bits
+ * (relative error <= 2^-22, an order below the fp32 rounding of the 2048-term dots that produce
+ * them), with half the exchange traffic.  32 carries every activation as a full fp32 with a
+ * 32-bit phase tag, as the reference's act buffer (kernels/drama.cu:493,516).  Other values ->
+ * -1.  The step keeps a running layer count in sync[2]. */
 int dr_step_set_act_exchange(int bits);
 
 /* Wait limit of the fused step's exchanges in microseconds (0 restores the default, 200000).

@@ -65,9 +65,10 @@ def check_stack(st, x0, idx, wts, sg, xs, x_final):
 
 
 @pytest.mark.parametrize("fmt,E,n,bits", [("cfg", 256, 3, 32), ("ref", 256, 2, 32), ("cfg", 64, 4, 32), ("cfg", 8, 2, 32),
-                                          ("cfg", 256, 3, 24), ("ref", 64, 2, 24)])
+                                          ("cfg", 256, 3, 30), ("ref", 64, 2, 30)])
 def test_step_matches_oracle_layer_by_layer(fmt, E, n, bits):
-    """bits: transport of the routed activations between workgroups (fp32, or 24-bit floats)."""
+    """bits: transport of the routed activations between workgroups (fp32 with a 32-bit tag, or
+    fp32 with the phase in the two low mantissa bits)."""
     print(f"step parity fmt={fmt} E={E} layers={n} act exchange {bits} bit", flush=True)
     st = Stack([300 + 7 * i for i in range(n)], E, fmt)
     x0 = np.random.default_rng(5).normal(0, 1, H).astype(np.float32)
@@ -77,13 +78,48 @@ def test_step_matches_oracle_layer_by_layer(fmt, E, n, bits):
     try:
         idx, wts, sg, xs = st.run(xd)
     finally:
-        L.dr_step_set_act_exchange(32)
+        L.dr_step_set_act_exchange(0)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"
     check_stack(st, x0, idx, wts, sg, xs, host(xd))
 
 
+def test_step_in_band_phase_over_launches_of_any_length():
+    """The in-band phase (act exchange 30) counts layers over launches of different lengths on
+    one ll / sync pair: one-layer launches (the engine's), then 3, 1, 2 layers; every launch's
+    routing and outputs against the oracle on its own input."""
+    import torch
+
+    st = Stack([700 + i for i in range(3)], 64, "cfg")
+    L = D.lib()
+    x0 = np.random.default_rng(9).normal(0, 1, H).astype(np.float32)
+    xd = dev(x0)
+    L.dr_step_set_act_exchange(30)
+    try:
+        for call, (first, n) in enumerate([(0, 1), (1, 1), (2, 1), (0, 1), (0, 3), (1, 1), (1, 2), (0, 1)]):
+            print(f"in-band phase launch {call}: layers {first}..{first + n - 1}", flush=True)
+            xin = host(xd).copy()
+            idx = torch.full((n * TOPK,), -1, dtype=torch.int32, device="cuda")
+            wts = torch.zeros(n * TOPK, device="cuda")
+            sg = torch.zeros(n, device="cuda")
+            xs = torch.zeros(n * H, device="cuda")
+            L.dr_moe_decode_step_bf16s(D.ptr(st.table) + 80 * first, n, D.ptr(xd), st.E, H, I, TOPK, 1e-6,
+                                       D.ptr(st.ll), D.ptr(st.sync), D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(xs),
+                                       D.stream_ptr())
+            torch.cuda.synchronize()
+            assert int(host(st.sync)[1]) == 0, "step reported a timeout"
+
+            class Sub:
+                h, E = st.h[first:first + n], st.E
+
+            check_stack(Sub, xin, host(idx).reshape(n, TOPK), host(wts).reshape(n, TOPK), host(sg),
+                        host(xs).reshape(n, H), host(xd))
+        assert int(host(st.sync)[2]) == 11, "running layer count"
+    finally:
+        L.dr_step_set_act_exchange(0)
+
+
 @pytest.mark.parametrize("fmt,E,n,bits", [("cfg", 32, 3, 32), ("ref", 16, 2, 32), ("cfg", 8, 2, 32), ("cfg", 16, 1, 32),
-                                          ("cfg", 32, 2, 24)])
+                                          ("cfg", 32, 2, 30)])
 def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n, bits):
     """Block-FP8 routed experts (dr_moe_decode_step_fp8*): the same routing and layer bar."""
     print(f"fp8 step parity fmt={fmt} E={E} layers={n} act exchange {bits} bit", flush=True)
@@ -95,7 +131,7 @@ def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n, bits):
     try:
         idx, wts, sg, xs = st.run(xd)
     finally:
-        L.dr_step_set_act_exchange(32)
+        L.dr_step_set_act_exchange(0)
     assert int(host(st.sync)[1]) == 0, "step reported a timeout"
     check_stack(st, x0, idx, wts, sg, xs, host(xd))
 
@@ -152,6 +188,7 @@ def test_step_without_norm_and_without_outputs(kind):
 
 def test_step_rejects_bad_shapes():
     assert D.lib().raw("dr_step_set_act_exchange")(16) == -1
+    assert D.lib().raw("dr_step_set_act_exchange")(24) == -1
     st = Stack([1], 16, "cfg")
     x = dev(np.zeros(H, np.float32))
     L = D.lib()

@@ -277,90 +277,9 @@ __global__ void __launch_bounds__(320)
   }
 }
 
-// Canonical bf16 GEMM C = A . W^T (+ beta C).  Block = 4 waves, 4 GM_MPW rows of A x GM_BN rows of W;
-// wave w holds GM_MPW rows of A (its lane chunks, as fp32) in registers, the block's GM_BN
-// W rows are staged once in LDS (each read by all four waves), and every dot is the canonical
-// one: lane l sums its chunks l + 64 j in element order, then the ascending xor tree.
-// NCH = chunks per lane.
-constexpr int GM_MPW = 2, GM_BN = 8;  // measured: 2 x 8 per wave 15 us, 4 x 8 20 us (300 x 257 x 2048)
-static_assert(GM_BN <= 8, "the W tile is staged as at most 2 NCH chunks per thread");
-
-template <int NCH>
-__global__ void __launch_bounds__(256)
-    k_gemm_canon(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W, float* __restrict__ C, int M,
-                 int N, int K, float beta) {
-  extern __shared__ uint4 wt[];  // [GM_BN][K / 8] chunks
-  const int lane = lane_id(), wave = wave_id();
-  const int m0 = (blockIdx.x * 4 + wave) * GM_MPW;
-  const int n0 = blockIdx.y * GM_BN;
-  const int KC = K / 8;
-  // W tile loads first (GM_BN KC <= 2 NCH x 256 chunks), then A, then the LDS stores
-  uint4 wv[2 * NCH];
-#pragma unroll
-  for (int i = 0; i < 2 * NCH; ++i) {
-    const int q = threadIdx.x + 256 * i, nn = q / KC, c = q - nn * KC;
-    wv[i] = q < GM_BN * KC && n0 + nn < N ? ld16(W + (size_t)(n0 + nn) * K + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
-  }
-  float a[GM_MPW][NCH * 8];
-#pragma unroll
-  for (int r = 0; r < GM_MPW; ++r) {
-    const int m = m0 + r < M ? m0 + r : M - 1;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + WAVE * j;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (c < KC) v = ld16(A + (size_t)m * K + (size_t)c * 8);
-      a[r][8 * j + 0] = bf16_lo(v.x), a[r][8 * j + 1] = bf16_hi(v.x);
-      a[r][8 * j + 2] = bf16_lo(v.y), a[r][8 * j + 3] = bf16_hi(v.y);
-      a[r][8 * j + 4] = bf16_lo(v.z), a[r][8 * j + 5] = bf16_hi(v.z);
-      a[r][8 * j + 6] = bf16_lo(v.w), a[r][8 * j + 7] = bf16_hi(v.w);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 2 * NCH; ++i) {
-    const int q = threadIdx.x + 256 * i;
-    if (q < GM_BN * KC) wt[q] = wv[i];
-  }
-  __syncthreads();
-  for (int nn = 0; nn < GM_BN; ++nn) {
-    const int n = n0 + nn;
-    if (n >= N) break;
-    uint4 w[NCH];
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + WAVE * j;
-      w[j] = c < KC ? wt[nn * KC + c] : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int r = 0; r < GM_MPW; ++r) {
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        if (lane + WAVE * j < KC) {
-          const float* av = &a[r][8 * j];
-          acc = __builtin_fmaf(bf16_lo(w[j].x), av[0], acc);
-          acc = __builtin_fmaf(bf16_hi(w[j].x), av[1], acc);
-          acc = __builtin_fmaf(bf16_lo(w[j].y), av[2], acc);
-          acc = __builtin_fmaf(bf16_hi(w[j].y), av[3], acc);
-          acc = __builtin_fmaf(bf16_lo(w[j].z), av[4], acc);
-          acc = __builtin_fmaf(bf16_hi(w[j].z), av[5], acc);
-          acc = __builtin_fmaf(bf16_lo(w[j].w), av[6], acc);
-          acc = __builtin_fmaf(bf16_hi(w[j].w), av[7], acc);
-        }
-      }
-      acc = wave_sum(acc);
-      const int m = m0 + r;
-      if (lane == 0 && m < M) {
-        float* c = C + (size_t)m * N + n;
-        *c = beta == 0.f ? acc : acc + beta * *c;
-      }
-    }
-  }
-}
-
 // The same canonical GEMM for few rows of A (M <= GR_MAXM, decode batches): one wave per W
 // row, which it loads once and dots with every A row (4 at a time, all loads issued first);
-// 8 waves per block.  Every dot has the canonical order, so C equals k_gemm_canon's bits.
+// 8 waves per block.  Every dot has the canonical order, so C equals k_gemm_tile's bits.
 constexpr int GR_MAXM = 16;
 template <int NCH>
 __global__ void __launch_bounds__(512)
@@ -414,14 +333,113 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+// The same canonical GEMM, one wave per 8 x 8 tile of C (4 tiles per block, no LDS): lane l
+// accumulates all 64 dots over its chunks l + 64 j in element order (the canonical lane sums),
+// then one reduce-scatter over the ascending xor tree finishes them together.  Step o pairs
+// lane l with l ^ o exactly as the canonical butterfly does, and each pair of lanes splits its
+// list of partial sums: the lane with bit o clear keeps the first half (adding its partner's
+// copy of it), the other the second half, so after the six steps lane l holds output
+// bitrev6(l) with the canonical tree's bits (a + b = b + a).  Exchanges: DPP quad_perm (o = 1,
+// 2) and row_ror (o = 4: by 12 for the lanes whose partner is l + 4, by 4 for l - 4; o = 8: by
+// 8), v_permlane16_swap / v_permlane32_swap (o = 16, 32; the swap itself hands each lane the
+// half it keeps).  A and W chunks of the next j are requested before the current j's FMAs.
+// Measured at 300 x 257 x 2048: 12.0 us (a 2 x 8 per-wave kernel with one butterfly per dot: 16.8 us); 4 x 8 tiles (twice the waves,
+// more conversions per FMA) 13.9 us.
+template <int O, int V>
+DEV void rs_step(float (&v)[64]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 0; k < V / 2; ++k) {
+    const float x = v[k], y = v[k + V / 2];
+    if constexpr (O >= 16) {
+      const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+      v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+      constexpr int cx = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x12C : 0x128;
+      constexpr int cy = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x124 : 0x128;
+      const float px = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), cx, 0xF, 0xF, false));
+      const float py = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y), cy, 0xF, 0xF, false));
+      v[k] = (lane & O) ? y + py : x + px;
+    }
+  }
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(256)
+    k_gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W, float* __restrict__ C, int M, int N,
+                int K, float beta) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int tn = (N + 7) >> 3;
+  const int tile = blockIdx.x * 4 + wave_id();
+  const int m0 = (tile / tn) * 8, n0 = (tile % tn) * 8;
+  if (m0 >= M) return;
+  const int KC = K / 8;
+  const uint16_t* ap[8];
+  const uint16_t* wp[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    ap[r] = A + (size_t)(m0 + r < M ? m0 + r : M - 1) * K + (size_t)lane * 8;
+    wp[r] = W + (size_t)(n0 + r < N ? n0 + r : N - 1) * K + (size_t)lane * 8;
+  }
+  float acc[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc[i] = 0.f;
+  uint4 ac[2][8], wc[2][8];
+  auto load = [&](int j, int b) {
+    const bool in = lane + WAVE * j < KC;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      ac[b][r] = in ? ld16(ap[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
+      wc[b][r] = in ? ld16(wp[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  load(0, 0);
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int b = j & 1;
+    if (j + 1 < NCH) load(j + 1, b ^ 1);
+    if (lane + WAVE * j < KC) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a[8], w[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const uint32_t aw = e < 2 ? ac[b][r].x : e < 4 ? ac[b][r].y : e < 6 ? ac[b][r].z : ac[b][r].w;
+          const uint32_t ww = e < 2 ? wc[b][r].x : e < 4 ? wc[b][r].y : e < 6 ? wc[b][r].z : wc[b][r].w;
+          a[r] = (e & 1) ? bf16_hi(aw) : bf16_lo(aw);
+          w[r] = (e & 1) ? bf16_hi(ww) : bf16_lo(ww);
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+#pragma unroll
+          for (int n = 0; n < 8; ++n) acc[8 * m + n] = __builtin_fmaf(w[n], a[m], acc[8 * m + n]);
+      }
+    }
+  }
+  rs_step<1, 64>(acc);
+  rs_step<2, 32>(acc);
+  rs_step<4, 16>(acc);
+  rs_step<8, 8>(acc);
+  rs_step<16, 4>(acc);
+  rs_step<32, 2>(acc);
+  const int i = (int)(__builtin_bitreverse32((uint32_t)lane) >> 26);
+  const int m = m0 + (i >> 3), n = n0 + (i & 7);
+  if (m < M && n < N) {
+    float* c = C + (size_t)m * N + n;
+    *c = beta == 0.f ? acc[0] : acc[0] + beta * *c;
+  }
+}
+
 template <int NCH>
 void launch_gemm(const uint16_t* A, const uint16_t* W, float* C, int M, int N, int K, float beta, hipStream_t st) {
   if (M <= GR_MAXM) {
     hipLaunchKernelGGL(k_gemm_rows<NCH>, dim3((N + 7) / 8), dim3(512), 0, st, A, W, C, M, N, K, beta);
     return;
   }
-  const dim3 g((M + 4 * GM_MPW - 1) / (4 * GM_MPW), (N + GM_BN - 1) / GM_BN);
-  hipLaunchKernelGGL(k_gemm_canon<NCH>, g, dim3(256), (size_t)GM_BN * (K / 8) * 16, st, A, W, C, M, N, K, beta);
+  const int tiles = ((M + 7) / 8) * ((N + 7) / 8);
+  hipLaunchKernelGGL(k_gemm_tile<NCH>, dim3((tiles + 3) / 4), dim3(256), 0, st, A, W, C, M, N, K, beta);
 }
 
 }  // namespace

@@ -51,6 +51,7 @@ constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
 constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll offsets are per format
+constexpr uint64_t ST_DEFER_SIBLING = 55;  // ticks after the layer start at which waves 4 and 5 begin the norm
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrealtime runs at 100 MHz: 0.2 s
 
 // slot arrays (64-bit words) inside the caller's ll buffer
@@ -233,7 +234,9 @@ template <class SC>
 struct StepQ4 {
   static constexpr bool kMinTerm = true;
   // first-poll offsets (measured; kOffX: 195 -> 12.3, 215-235 -> 11.6-11.8, 285 -> 12.2 us/layer)
-  static constexpr uint32_t kOffL = 185, kOffAct = 370, kOffX = 215;
+  // (kOffL: 185 before the router waves had their SIMDs to themselves; 115 -> 11.8, 130 -> 11.4,
+  // 140-160 -> 11.15-11.2 us/layer)
+  static constexpr uint32_t kOffL = 145, kOffAct = 370, kOffX = 215;
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
   // 400 -> 11.5 us/layer)
   static constexpr uint32_t kOffActIb = 375;
@@ -322,7 +325,8 @@ struct StepFP8 {
   static constexpr bool kMinTerm = false;
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
-  static constexpr uint32_t kOffL = 185, kOffAct = 430, kOffX = 165;
+  // (kOffL: 135-160 -> 11.36-11.41, 185 -> 11.66 us/layer)
+  static constexpr uint32_t kOffL = 150, kOffAct = 430, kOffX = 165;
   // in-band activation phase: 400 -> 12.6, 430 -> 11.8, 460-470 -> 11.7, 510 -> 12.0 us/layer
   static constexpr uint32_t kOffActIb = 465;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
@@ -493,11 +497,17 @@ __global__ void __launch_bounds__(ST_NT, 1)
     // ---- RMSNorm (canonical, every wave) and the router row; the poller collects logits
     {
       res = reinterpret_cast<const float*>(xr4)[n];
+      // waves 4 and 5 share SIMDs 0 and 1 with the router waves (wave 0, and wave 1 of block 0):
+      // they start their norm once the router rows are out (measured: the logits can then be
+      // polled 0.4 us earlier, 11.5 -> 11.15 us/layer)
+      if (wave == 4 || wave == 5) wait_until(t_layer + ST_DEFER_SIBLING);
       float4 xr[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) xr[j] = xr4[lane + 64 * j];
       const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
-      {
+      // this thread's slot of the normalised x (and the int4 chunk sums), needed from gate_up on;
+      // the router waves do it after their router row
+      auto stage_xq = [&]() {
         const float4 xn = canon_norm4(xr4[tid], inv, nwv);
         xq4[F::xslot(tid)] = xn;
         if constexpr (F::kMinTerm) {
@@ -505,7 +515,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
           t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
           if ((lane & 7) == 0) s_xsum[tid >> 3] = t;
         }
-      }
+      };
+      if (!is_router) stage_xq();
       if (is_router) {
         float4 a[4], b[4];
 #pragma unroll
@@ -516,6 +527,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
         }
         const float acc = canon_row_dot<4>(rw.w, a, b);
         if (lane == 0) ll_put(ll + LL_LOG + rrow, acc, tA);
+        stage_xq();
       }
       // shared gate_up pair (waves 2 and 6): needs only the normalised x, so it runs here,
       // inside the logits exchange, instead of after top-k

@@ -236,10 +236,12 @@ struct StepQ4 {
   // first-poll offsets (measured; kOffX: 195 -> 12.3, 215-235 -> 11.6-11.8, 285 -> 12.2 us/layer)
   // (kOffL: 185 before the router waves had their SIMDs to themselves; 115 -> 11.8, 130 -> 11.4,
   // 140-160 -> 11.15-11.2 us/layer)
-  static constexpr uint32_t kOffL = 145, kOffAct = 370, kOffX = 215;
+  // (kOffX, with the in-band activation phase and kOffActIb 375-385: 175 -> 11.0, 185-195 -> 10.85-10.95,
+  // 215 -> 11.1 us/layer)
+  static constexpr uint32_t kOffL = 145, kOffAct = 370, kOffX = 190;
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
   // 400 -> 11.5 us/layer)
-  static constexpr uint32_t kOffActIb = 375;
+  static constexpr uint32_t kOffActIb = 380;
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -326,7 +328,7 @@ struct StepFP8 {
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
   // (kOffL: 135-160 -> 11.36-11.41, 185 -> 11.66 us/layer)
-  static constexpr uint32_t kOffL = 150, kOffAct = 430, kOffX = 165;
+  static constexpr uint32_t kOffL = 150, kOffAct = 430, kOffX = 155;  // (kOffX 140-165: 11.2-11.3 us/layer)
   // in-band activation phase: 400 -> 12.6, 430 -> 11.8, 460-470 -> 11.7, 510 -> 12.0 us/layer
   static constexpr uint32_t kOffActIb = 465;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }

@@ -233,6 +233,9 @@ struct SpecAct {
 template <class SC>
 struct StepQ4 {
   static constexpr bool kMinTerm = true;
+  // gate_up loads issued straight from the merge's ranks, before the picks go through LDS
+  // (10.87 -> 10.68 us/layer; the FP8 policy measured 11.2 -> 14.4 with it and keeps the LDS path)
+  static constexpr bool kEarlyGu = true;
   // first-poll offsets (measured; kOffX: 195 -> 12.3, 215-235 -> 11.6-11.8, 285 -> 12.2 us/layer)
   // (kOffL: 185 before the router waves had their SIMDs to themselves; 115 -> 11.8, 130 -> 11.4,
   // 140-160 -> 11.15-11.2 us/layer)
@@ -241,7 +244,7 @@ struct StepQ4 {
   static constexpr uint32_t kOffL = 145, kOffAct = 370, kOffX = 190;
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
   // 400 -> 11.5 us/layer)
-  static constexpr uint32_t kOffActIb = 380;
+  static constexpr uint32_t kOffActIb = 345;  // (335-350 with the early gate_up loads: 10.7 us/layer)
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -325,6 +328,7 @@ struct StepQ4 {
 template <int SF>
 struct StepFP8 {
   static constexpr bool kMinTerm = false;
+  static constexpr bool kEarlyGu = false;
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
   // (kOffL: 135-160 -> 11.36-11.41, 185 -> 11.66 us/layer)
@@ -579,13 +583,23 @@ __global__ void __launch_bounds__(ST_NT, 1)
 
     // ---- top-k, second half: the 32 candidates ranked by every wave (no second barrier);
     // lane k < 8 of each wave's s_sel row receives pick k
+    typename F::GU gu;
+    int my_idx;
     {
       const int rk8 = canon_merge_rank32(s_cand);
-      if (lane < 32 && rk8 < ST_TOPK) s_sel[wave][rk8] = canon_cand64_expert(s_cand[lane]);
+      const int my_e = canon_cand64_expert(s_cand[lane & 31]);
+      if constexpr (F::kEarlyGu) {
+        // ---- routed weight loads: gate_up pairs of expert slot rk, whose expert the lane
+        // holding the candidate of rank rk hands over (no LDS round trip before the loads)
+        const uint64_t hit = __ballot(lane < 32 && rk8 == rk);
+        const size_t ek = (size_t)__builtin_amdgcn_readlane(my_e, hit ? (int)__builtin_ctzll(hit) : 0);
+        F::load_gu(Ly, ek, rj, lane, gu);
+      }
+      if (lane < 32 && rk8 < ST_TOPK) s_sel[wave][rk8] = my_e;
+      my_idx = s_sel[wave][lane & (ST_TOPK - 1)];
     }
 
     {
-      const int my_idx = s_sel[wave][lane & (ST_TOPK - 1)];
       // the next layer's record: a scalar load issued here returns while the gate_up loads
       // are in flight (read at the activation barrier it would cost a round trip on the way
       // to the residual publish; at the layer start its wait would hold up the router's LDS
@@ -593,11 +607,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       Ln = layers[l + 1 < L ? l + 1 : l];
       ST_MARK(3);
       const uint64_t t_topk = __builtin_amdgcn_s_memrealtime();
-
-      // ---- routed weight loads: gate_up pairs, then the down row (8 experts + shared)
-      const size_t ek = (size_t)__builtin_amdgcn_readlane(my_idx, rk);
-      typename F::GU gu;
-      F::load_gu(Ly, ek, rj, lane, gu);
+      if constexpr (!F::kEarlyGu) F::load_gu(Ly, (size_t)__builtin_amdgcn_readlane(my_idx, rk), rj, lane, gu);
       // routing weights, needed only by the down phase: every wave computes the softmax
       // denominator and its pick weights while its gate_up loads are in flight
       __builtin_amdgcn_sched_barrier(0);

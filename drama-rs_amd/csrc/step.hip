@@ -241,7 +241,9 @@ struct StepQ4 {
   // 140-160 -> 11.15-11.2 us/layer)
   // (kOffX, with the in-band activation phase and kOffActIb 375-385: 175 -> 11.0, 185-195 -> 10.85-10.95,
   // 215 -> 11.1 us/layer)
-  static constexpr uint32_t kOffL = 145, kOffAct = 370, kOffX = 190;
+  static constexpr uint32_t kOffL = 145, kOffAct = 355, kOffX = 190;
+  static constexpr uint32_t kOffXA32 = 235;  // residual offset with the full-fp32 activation exchange
+                                             // (190 -> 11.95, 215 -> 11.6-11.7, 235 -> 11.5 us/layer)
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
   // 400 -> 11.5 us/layer)
   static constexpr uint32_t kOffActIb = 345;  // (335-350 with the early gate_up loads: 10.7 us/layer)
@@ -333,6 +335,7 @@ struct StepFP8 {
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
   // (kOffL: 135-160 -> 11.36-11.41, 185 -> 11.66 us/layer)
   static constexpr uint32_t kOffL = 150, kOffAct = 430, kOffX = 155;  // (kOffX 140-165: 11.2-11.3 us/layer)
+  static constexpr uint32_t kOffXA32 = 165;
   // in-band activation phase: 400 -> 12.6, 430 -> 11.8, 460-470 -> 11.7, 510 -> 12.0 us/layer
   static constexpr uint32_t kOffActIb = 465;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
@@ -704,7 +707,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
       ST_MARK(6);
       // ---- residual exchange for the next layer (every wave read its x[n] at the layer start)
       if (poller && l + 1 < L) {
-        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + F::kOffX, tmo);
+        const uint32_t r = poll_wave<4, ST_NP>(ll + LL_X, pw, Spec32{tC, H, reinterpret_cast<float*>(xr4)}, sync, t_act + (A32 ? F::kOffXA32 : F::kOffX), tmo);
         if (!r && lane == 0) s_abort = 1;
         ST_PUT(10, r);
       }

@@ -591,6 +591,11 @@ __global__ void __launch_bounds__(ST_NT, 1)
     {
       const int rk8 = canon_merge_rank32(s_cand);
       const int my_e = canon_cand64_expert(s_cand[lane & 31]);
+      // the next layer's record: a scalar load, issued ahead of the gate_up loads (behind them
+      // its return, which the LDS reads below wait for too, queues behind the weight stream);
+      // read at the activation barrier it would cost a round trip on the way to the residual
+      // publish, and at the layer start its wait would hold up the router's LDS reads
+      Ln = layers[l + 1 < L ? l + 1 : l];
       if constexpr (F::kEarlyGu) {
         // ---- routed weight loads: gate_up pairs of expert slot rk, whose expert the lane
         // holding the candidate of rank rk hands over (no LDS round trip before the loads)
@@ -603,11 +608,6 @@ __global__ void __launch_bounds__(ST_NT, 1)
     }
 
     {
-      // the next layer's record: a scalar load issued here returns while the gate_up loads
-      // are in flight (read at the activation barrier it would cost a round trip on the way
-      // to the residual publish; at the layer start its wait would hold up the router's LDS
-      // reads, which share the counter)
-      Ln = layers[l + 1 < L ? l + 1 : l];
       ST_MARK(3);
       const uint64_t t_topk = __builtin_amdgcn_s_memrealtime();
       if constexpr (!F::kEarlyGu) F::load_gu(Ly, (size_t)__builtin_amdgcn_readlane(my_idx, rk), rj, lane, gu);

@@ -110,7 +110,9 @@ class Prefill:
         self.idx, self.wts, self.sg = z(n, torch.int32), z(n), z(rows)
         self.sact, self.sh = z(rows * I, torch.int16), z(rows * H)
         self.counts, self.offsets, self.slot_of = z(E, torch.int32), z(E, torch.int32), z(n, torch.int32)
-        self.xp, self.act, self.yp = z(n * H, torch.int16), z(n * I, torch.int16), z(n * H)
+        self.row_of_slot, self.counter = z(n + 16, torch.int32), z(4, torch.int32)
+        self.act, self.yp = z(n * I, torch.int16), z(n * H)
+        self.grouped = False  # set by router(): top-k came with its grouping
         h = ctypes.c_void_p()
         D.lib().dr_cublas_create(ctypes.byref(h), self.sp)
         self.h = h.value
@@ -134,17 +136,22 @@ class Prefill:
     def router(self, lib, L):
         P = D.ptr
         lib.dr_gemm(self.h, P(self.hn), P(L["router"]), P(self.logits), self.rows, E + 1, H, 0.0)
-        lib.dr_moe_topk(P(self.logits), self.rows, E, TOPK, E + 1, P(self.idx), P(self.wts), P(self.sg), self.sp)
+        lib.dr_moe_topk_group(P(self.logits), self.rows, E, TOPK, E + 1, P(self.idx), P(self.wts), P(self.sg),
+                              P(self.counts), P(self.offsets), P(self.slot_of), P(self.row_of_slot), P(self.counter),
+                              self.sp)
+        self.grouped = True
 
     def experts(self, lib, L, fp8=False, shared_started=False):
         P, sp = D.ptr, self.sp
         if not shared_started:
             self.shared_begin(lib, L)
-        lib.dr_moe_group(P(self.idx), self.n, E, P(self.counts), P(self.offsets), P(self.slot_of), sp)
-        lib.dr_moe_gather_rows(P(self.slot_of), self.rows, TOPK, P(self.hn), P(self.xp), H, sp)
-        f = lib.dr_moe_prefill_fp8_bf16s if fp8 else lib.dr_moe_prefill_bf16s
-        f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.xp), P(self.offsets), P(self.counts), P(self.act),
-          P(self.yp), E, H, I, sp)
+        if not self.grouped:  # a routing given from outside (the skewed variant)
+            lib.dr_moe_group_rows(P(self.idx), self.rows, TOPK, E, P(self.counts), P(self.offsets), P(self.slot_of),
+                                  P(self.row_of_slot), sp)
+        self.grouped = False
+        f = lib.dr_moe_prefill_rows_fp8_bf16s if fp8 else lib.dr_moe_prefill_rows_bf16s
+        f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.hn), self.rows, P(self.row_of_slot),
+          P(self.offsets), P(self.counts), P(self.act), P(self.yp), E, H, I, sp)
         if self.overlap:
             self.st.wait_event(self.ev_join)
         lib.dr_moe_combine(P(self.x), P(self.yp), P(self.slot_of), P(self.wts), P(self.sg), P(self.sh), self.rows, TOPK,
@@ -155,8 +162,7 @@ class Prefill:
         per_expert = sum(L[k].numel() * L[k].element_size() for k in ("gu_q", "gu_s", "d_q", "d_s")) // E
         shared = sum(L[k].numel() * L[k].element_size() for k in ("sgu_q", "sgu_s", "sd_q", "sd_s"))
         r, n = self.rows, self.n
-        acts = (r * H * 2 * 3          # hn read by router, shared and gather
-                + n * H * 2 * 2        # xp written and read
+        acts = (r * H * 2 * 3          # hn read by router, shared expert and gate_up
                 + n * I * 2 * 2        # act written and read
                 + n * H * 4 * 2        # yp written and read
                 + r * I * 2 * 2 + r * H * 4 * 2  # shared act / out
@@ -181,7 +187,7 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
     cnt = pf.counts.cpu()
     uniform = rec(ms * 1000, nbytes, experts_hit=hit, rows_per_expert_max=int(cnt.max()), pairs=pf.n,
                   us_graph=round(msg * 1000, 2),
-                  note="router GEMM + top-k + group + gather + grouped GEMM + combine" + (
+                  note="router GEMM + top-k with grouping + grouped GEMM (token rows read through the slot map) + combine" + (
                       ", the shared expert on a second stream beside them" if pf.overlap else " + shared, one stream")
                        + "; us_graph: replayed from a HIP graph")
     # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
@@ -336,8 +342,8 @@ def config5_fp8(lib, st, iters=100, copies=4):
     ms4g = timed_graph(b4, iters, st, copies)
     nb4, hit = pf.layer_bytes(L)
     out["decode_batch4_grouped"] = rec(ms4 * 1000, nb4, experts_hit=hit, us_graph=round(ms4g * 1000, 2),
-                                       note="4 rows via the prefill path (router GEMM, top-k, grouping, gather, "
-                                            "grouped MFMA GEMM, combine: 9 launches); us_graph: from a HIP graph")
+                                       note="4 rows via the prefill path (router GEMM, top-k with grouping, "
+                                            "grouped MFMA GEMMs, combine: 7 launches); us_graph: from a HIP graph")
     # the small-batch decode path: router + top-k for the 4 rows in one launch, then the batch-1
     # chain's expert kernels over the 4 rows (3 launches)
     x4 = torch.randn(4, H, device="cuda")

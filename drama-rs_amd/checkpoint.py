@@ -245,7 +245,7 @@ class MoeStack:
         rows = x.shape[0]
         H, E, I, k = self.H, self.E, self.I, self.topk
         if chunk * k > 8192:
-            raise ValueError("chunk * topk must be <= 8192 (the pairs dr_moe_group sorts in one call)")
+            raise ValueError("chunk * topk must be <= 8192 (the pairs dr_moe_topk_group sorts in one call)")
         c = min(chunk, rows)
         dev = x.device
         # temporaries come from the caching allocator of the stream the kernels run on, so they
@@ -257,10 +257,11 @@ class MoeStack:
             logits, idx, wts, sg = z(c * (E + 1)), z(c * k, torch.int32), z(c * k), z(c)
             sact, sh = z(c * I, torch.int16), z(c * H)
             counts, offsets, slot_of = z(E, torch.int32), z(E, torch.int32), z(c * k, torch.int32)
-            xp, act, yp = z(c * k * H, torch.int16), z(c * k * I, torch.int16), z(c * k * H)
+            row_of_slot, counter = z(c * k + 16, torch.int32), torch.zeros(4, dtype=torch.int32, device=dev)
+            act, yp = z(c * k * I, torch.int16), z(c * k * H)
         gh = self._gemm_handle(st)
-        # the shared expert needs only hn, so it runs on a second stream beside the routing,
-        # grouping and gather and joins before the combine.  Only from a created stream: events
+        # the shared expert needs only hn, so it runs on a second stream beside the routing and
+        # grouping and joins before the combine.  Only from a created stream: events
         # recorded through a wrapper of the null stream (handle 0) did not order the kernels
         # launched on it (measured: chunk k + 1's shared output overwrote chunk k's before its
         # combine), so on the null stream everything stays in order on it.
@@ -279,12 +280,13 @@ class MoeStack:
             if overlap:
                 join.record(side)
             lib.dr_gemm(gh, P(hr), P(L["router"]), P(logits), n, E + 1, H, 0.0)
-            lib.dr_moe_topk(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), st)
-            lib.dr_moe_group(P(idx), n * k, E, P(counts), P(offsets), P(slot_of), st)
-            lib.dr_moe_gather_rows(P(slot_of), n, k, P(hr), P(xp), H, st)
-            pf = lib.dr_moe_prefill_fp8 if self.fp8 else lib.dr_moe_prefill
-            pf(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(xp), P(offsets), P(counts), P(act), P(yp), E,
-               H, I, st)
+            # top-k and the grouping in one launch; the grouped GEMM reads its token rows from hn
+            # through row_of_slot (no gathered copy)
+            lib.dr_moe_topk_group(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), P(counts), P(offsets),
+                                  P(slot_of), P(row_of_slot), P(counter), st)
+            pf = lib.dr_moe_prefill_rows_fp8 if self.fp8 else lib.dr_moe_prefill_rows
+            pf(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(hr), n, P(row_of_slot), P(offsets), P(counts),
+               P(act), P(yp), E, H, I, st)
             if overlap:
                 main.wait_event(join)
             lib.dr_moe_combine(P(xr), P(yp), P(slot_of), P(wts), P(sg), P(sh), n, k, H, st)

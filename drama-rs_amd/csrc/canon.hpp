@@ -208,6 +208,15 @@ DEV int canon_merge_rank32(const uint64_t* __restrict__ cand) {
   return __float_as_int(a) + __float_as_int(b);
 }
 
+// Pick k < topk <= 8 of the 32 group candidates, by rank (canon_merge_rank32): the candidate
+// of rank k is written to sel[k] and read back by lane k.  One wave, all lanes active.
+DEV int merge_picks(const uint64_t* cand, int* sel, int topk) {
+  const int lane = lane_id();
+  const int rk = canon_merge_rank32(cand);
+  if (lane < 32 && rk < topk) sel[rk] = canon_cand64_expert(cand[lane]);
+  return lane < topk ? sel[lane] : 0;
+}
+
 // Softmax denominator: m = max of the non-NaN logits, z = sum of canon_exp(l - m) with lane
 // l summing experts l + 64 j in order, then the xor butterfly.  Same bits on every lane.
 DEV float canon_softmax_z(const float* __restrict__ l, int E, float* m_out) {

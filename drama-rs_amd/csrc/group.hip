@@ -10,7 +10,7 @@
 //   3. slot = offsets[e] + base[chunk][e] + rank.
 // The order within an expert is ascending pair index (the reference's atomics give an
 // unspecified order; this is one of its possible outcomes, and the CPU oracle's).
-#include "common.hpp"
+#include "canon.hpp"
 
 using namespace drm;
 
@@ -31,11 +31,14 @@ DEV uint64_t match8(uint32_t key, bool valid) {
   return m;
 }
 
-// mode 0: compute counts/offsets and slots; mode 1 (dr_moe_permute): offsets given, fill holds
-// the pairs of each expert already placed by earlier segments and is advanced by this one
-__global__ void __launch_bounds__(GR_THREADS)
-    k_group(const int* __restrict__ idx, int n, int E, int* __restrict__ counts, int* __restrict__ offsets,
-            int* __restrict__ slot_of, int mode, int* __restrict__ fill) {
+// The counting sort of one workgroup of GR_THREADS threads over pairs 0..n-1 whose expert ids
+// ld(i) returns.  mode 0: compute counts/offsets and slots; mode 1 (dr_moe_permute): offsets
+// given, fill holds the pairs of each expert already placed by earlier segments and is advanced
+// by this one.  row_of_slot (nullable): the inverse map slot -> pair i / topk.
+template <class Ld>
+DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* __restrict__ offsets,
+                     int* __restrict__ slot_of, int mode, int* __restrict__ fill, int* __restrict__ row_of_slot,
+                     int topk) {
   __shared__ uint16_t tab[GR_MAXCH][256];  // per-chunk count, then per-chunk base
   __shared__ uint8_t rank[GR_MAXN];
   __shared__ int s_off[256];
@@ -48,7 +51,7 @@ __global__ void __launch_bounds__(GR_THREADS)
     for (int h = 0; h < 2; ++h) {
       const int i = c * GR_CHUNK + h * 64 + lane;
       const bool valid = i < n;
-      const uint32_t key = valid ? (uint32_t)idx[i] & 255u : 0u;  // ids must be < E <= 256
+      const uint32_t key = valid ? (uint32_t)ld(i) & 255u : 0u;  // ids must be < E <= 256
       const uint64_t m = match8(key, valid);
       const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
       const int r = __popcll(m & lower);
@@ -102,9 +105,80 @@ __global__ void __launch_bounds__(GR_THREADS)
   }
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += GR_THREADS) {
-    const int e = idx[i] & 255, c = i / GR_CHUNK;
-    slot_of[i] = s_off[e] + (int)tab[c][e] + (int)rank[i];
+    const int e = ld(i) & 255, c = i / GR_CHUNK;
+    const int slot = s_off[e] + (int)tab[c][e] + (int)rank[i];
+    slot_of[i] = slot;
+    if (row_of_slot) row_of_slot[slot] = i / topk;
   }
+}
+
+__global__ void __launch_bounds__(GR_THREADS)
+    k_group(const int* __restrict__ idx, int n, int E, int* __restrict__ counts, int* __restrict__ offsets,
+            int* __restrict__ slot_of, int mode, int* __restrict__ fill, int* __restrict__ row_of_slot, int topk) {
+  group_block([&](int i) { return idx[i]; }, n, E, counts, offsets, slot_of, mode, fill, row_of_slot, topk);
+}
+
+// Prefill top-k and grouping in one launch.  Each block of 16 waves takes 3 rows (waves 5 s ..
+// 5 s + 4 for row 3 b + s: four 64-expert group selections and the softmax denominator, then the
+// rank merge, as k_moe_topk), publishes idx with cache-bypassing stores and counts itself in
+// once they have completed; the last block runs the stable counting sort of dr_moe_group over
+// all rows * topk pairs (reading idx back with cache-bypassing loads), writes counts, offsets,
+// slot_of and the inverse map row_of_slot, and resets the counter.
+constexpr int TG_ROWS = 3;
+__global__ void __launch_bounds__(GR_THREADS)
+    k_moe_topk_group(const float* __restrict__ logits, int rows, int E, int topk, int stride, int* __restrict__ idx,
+                     float* __restrict__ wts, float* __restrict__ sgate, int* __restrict__ counts,
+                     int* __restrict__ offsets, int* __restrict__ slot_of, int* __restrict__ row_of_slot,
+                     uint32_t* __restrict__ counter) {
+  __shared__ float lg[TG_ROWS][257];
+  __shared__ uint64_t s_cand[TG_ROWS][32];
+  __shared__ int s_sel[TG_ROWS][8];
+  __shared__ float s_mz[TG_ROWS][2];
+  __shared__ int s_last;
+  const int lane = lane_id(), wave = wave_id();
+  const int sub = wave / 5, w5 = wave % 5, r = blockIdx.x * TG_ROWS + sub;
+  const bool active = sub < TG_ROWS && r < rows;
+  for (int i = threadIdx.x; i < TG_ROWS * (E + 1); i += GR_THREADS) {
+    const int s = i / (E + 1), e = i - s * (E + 1), rr = blockIdx.x * TG_ROWS + s;
+    if (rr < rows) lg[s][e] = logits[(size_t)rr * stride + e];
+  }
+  __syncthreads();
+  if (active && topk <= 8) {
+    if (w5 < 4) {
+      int ck, ce;
+      canon_select_group8(lg[sub], E, w5, &ck, &ce);
+      if (lane < 8) s_cand[sub][w5 * 8 + lane] = canon_cand64(ck, ce);
+    } else {
+      float m;
+      const float z = canon_softmax_z(lg[sub], E, &m);
+      if (lane == 0) s_mz[sub][0] = m, s_mz[sub][1] = z;
+    }
+  }
+  __syncthreads();
+  if (active && w5 == 0) {
+    int id;
+    float w;
+    if (topk <= 8) {
+      id = merge_picks(s_cand[sub], s_sel[sub], topk);
+      w = canon_topk_weight(lg[sub][lane < topk ? id : 0], s_mz[sub][0], s_mz[sub][1], topk);
+    } else {
+      canon_softmax_topk(lg[sub], E, topk, &id, &w);
+    }
+    if (lane < topk) {
+      __hip_atomic_store(idx + (size_t)r * topk + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wts[(size_t)r * topk + lane] = w;
+    }
+    if (lane == 0) sgate[r] = lg[sub][E];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  group_block([&](int i) { return __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
+              rows * topk, E, counts, offsets, slot_of, 0, nullptr, row_of_slot, topk);
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // xp[slot_of[i]] = x[i / topk]: 16 bytes per thread, one pair per 256-thread block.
@@ -174,7 +248,28 @@ __global__ void k_swiglu_rows(const float* __restrict__ h, uint16_t* __restrict_
 
 API int dr_moe_group(const int* idx, int n, int E, int* counts, int* offsets, int* slot_of, hipStream_t st) {
   if (n < 0 || n > GR_MAXN || E < 1 || E > 256) return -1;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, E, counts, offsets, slot_of, 0, nullptr);
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, E, counts, offsets, slot_of, 0, nullptr,
+                     nullptr, 1);
+  return 0;
+}
+
+API int dr_moe_group_rows(const int* idx, int rows, int topk, int E, int* counts, int* offsets, int* slot_of,
+                         int* row_of_slot, hipStream_t st) {
+  if (rows < 0 || topk < 1 || (long long)rows * topk > GR_MAXN || E < 1 || E > 256 || !row_of_slot) return -1;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, rows * topk, E, counts, offsets, slot_of, 0,
+                     nullptr, row_of_slot, topk);
+  return 0;
+}
+
+API int dr_moe_topk_group(const float* logits, int rows, int E, int topk, int stride, int* idx, float* wts,
+                         float* sgate, int* counts, int* offsets, int* slot_of, int* row_of_slot, uint32_t* counter,
+                         hipStream_t st) {
+  if (E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E || stride < E + 1 || rows < 0 ||
+      (long long)rows * topk > GR_MAXN || !counter)
+    return -1;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(k_moe_topk_group, dim3((rows + TG_ROWS - 1) / TG_ROWS), dim3(GR_THREADS), 0, st, logits, rows, E,
+                     topk, stride, idx, wts, sgate, counts, offsets, slot_of, row_of_slot, counter);
   return 0;
 }
 
@@ -204,7 +299,7 @@ API int dr_moe_permute(const int* idx, int rows, int topk, const int* offsets, i
   for (int s0 = 0; s0 < n; s0 += GR_MAXN) {
     const int m = n - s0 < GR_MAXN ? n - s0 : GR_MAXN;
     hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx + s0, m, 256, nullptr,
-                       const_cast<int*>(offsets), slot_of + s0, 1, fill);
+                       const_cast<int*>(offsets), slot_of + s0, 1, fill, nullptr, 1);
   }
   hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(256), 0, st, slot_of, topk, x, xp, H);
   return 0;

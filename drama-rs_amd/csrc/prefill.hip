@@ -183,6 +183,30 @@ struct TokTile {
       v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (t * K + r * 8) * 2, 0, 0));
     }
   }
+  // The same tile with its rows gathered through a slot -> row map: token t of the pass is row
+  // rmap[row0 + t] of X (x_rows rows).  The 16 indices come with scalar loads (their wait does
+  // not queue behind the weight loads in flight), rows past ntok read zeros.  K / 8 = NT / 2:
+  // thread b's blocks belong to tokens 2 i and 2 i + 1.
+  DEV void load_rows(const uint16_t* __restrict__ X, int x_rows, const int* __restrict__ rmap, size_t row0,
+                     int ntok) {
+    static_assert(NT == 2 * (K / 8), "two tokens per block index");
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), 0, x_rows * K * 2, 0x00020000);
+    const __attribute__((address_space(4))) int* rp =
+        (const __attribute__((address_space(4))) int*)(rmap + row0);
+    int rr[PF_TOK];
+#pragma unroll
+    for (int t = 0; t < PF_TOK; ++t) rr[t] = rp[t];
+    const bool hi = threadIdx.x >= NT / 2;
+    const int r = threadIdx.x % (K / 8);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int t = 2 * i + (hi ? 1 : 0);
+      const int row = hi ? rr[2 * i + 1] : rr[2 * i];
+      const uint32_t off = t < ntok ? (uint32_t)((row * K + r * 8) * 2) : 0x7ffffff0u;
+      v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+  }
   // with_sums: also the fp32 sum of every 64-input group of every token, at float index
   // PF_TOK K / 2 + 16 G + t (after the tile), for the min term of the int4 format
   DEV void store(uint4* xs, bool with_sums) const {
@@ -260,11 +284,12 @@ DEV uint4 q4_frag(uint32_t w, uint32_t m, uint32_t b) {
 // B = weights (lane: row l % 16), so D[token 4 (l / 16) + i][row l % 16] sits in lane l: one
 // weight row per lane, one (scale, min) pair per group.  The group input sums X_g come from an
 // MFMA against bf16 ones (int4: staged with the tokens).
-template <class F, int MODE, int K>
+template <class F, int MODE, int K, bool GATHER>
 __global__ void __launch_bounds__(PF_GWPB * 64)
     k_grouped(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
               const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
-              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int E, uint32_t* __restrict__ err) {
+              size_t expert_q_bytes, size_t expert_s_elems, int s_elem_bytes, int E, uint32_t* __restrict__ err,
+              const int* __restrict__ rmap, int x_rows) {
   extern __shared__ uint4 xs[];  // two tile buffers of BUF blocks, the item table, the up hand-over
   constexpr int BUF = PF_TOK * K / 8 + (F::paired ? (K / 64) * PF_TOK / 4 : 0);
   constexpr int WR = MODE == 0 ? PF_GWPB / 2 : PF_GWPB;  // row tiles per item (per row set)
@@ -392,7 +417,8 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   __shared__ uint32_t n_stored, n_done, n_up, n_gate;
   if (threadIdx.x == 0) n_stored = 0, n_done = 0, n_up = 0, n_gate = 0;
   {
-    tt.load(X, cur.row0, cur.ntok);
+    if constexpr (GATHER) tt.load_rows(X, x_rows, rmap, cur.row0, cur.ntok);
+    else tt.load(X, cur.row0, cur.ntok);
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) fetch(cur, d, ring[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -510,7 +536,10 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
       // stored into the other tile buffer at mid-item, once every wave finished item k - 1
       // (the buffer's previous tile); after the block's last item nxt is the first item again
       // (loads and stores no one uses): branch-free, so the load counter stays exact
-      if (i == 0) tt.load(X, nxt.row0, nxt.ntok);
+      if (i == 0) {
+        if constexpr (GATHER) tt.load_rows(X, x_rows, rmap, nxt.row0, nxt.ntok);
+        else tt.load(X, nxt.row0, nxt.ntok);
+      }
       if (i + DEPTH < NS) {
         fetch(cur, i + DEPTH, ring[b]);
       } else {
@@ -850,7 +879,7 @@ inline int resident_blocks(const void* kern, int threads, size_t lds) {
 template <class F>
 void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const int* offsets, const int* counts,
                     void* out, int E, int N, int K, int mode, size_t eq, size_t es, int sb, int fixed_rows,
-                    hipStream_t st) {
+                    hipStream_t st, const int* rmap = nullptr, int x_rows = 0) {
   const int rows_out = mode == 0 ? N / 2 : N;
   if (fixed_rows >= 0) {
     // one weight set over all rows (the shared expert).  gate_up: the K-split kernel, one
@@ -872,19 +901,22 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
   // work items (expert, token pass, row block) the kernel derives from counts
   const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
                      (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0);
-  auto kern = mode == 0 ? k_grouped<F, 0, 2048> : k_grouped<F, 1, 512>;
+  auto kern = mode == 1 ? k_grouped<F, 1, 512, false> : rmap ? k_grouped<F, 0, 2048, true> : k_grouped<F, 0, 2048, false>;
   int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E,
-                     err_word());
+                     err_word(), rmap, x_rows);
 }
 
-// gate_up then down for all experts of a grouped batch
+// gate_up then down for all experts of a grouped batch; with rmap, the gate_up token rows are
+// read from X (x_rows rows) through the slot -> row map instead of from a gathered xp
 template <class F>
 int moe_prefill(const uint8_t* gu_q, const void* gu_s, const uint8_t* d_q, const void* d_s, const uint16_t* xp,
                 const int* offsets, const int* counts, uint16_t* act, float* y, int E, int H, int I, size_t gu_q_b,
-                size_t gu_s_e, size_t d_q_b, size_t d_s_e, int sb, hipStream_t st) {
+                size_t gu_s_e, size_t d_q_b, size_t d_s_e, int sb, hipStream_t st, const int* rmap = nullptr,
+                int x_rows = 0) {
   if (H != 2048 || I != 512 || E < 1 || E > PF_MAXE) return -1;
-  launch_grouped<F>(gu_q, gu_s, xp, offsets, counts, act, E, 2 * I, H, 0, gu_q_b, gu_s_e, sb, -1, st);
+  if (rmap && (x_rows < 1 || (long long)x_rows * H * 2 > 0x7fffffffll)) return -1;
+  launch_grouped<F>(gu_q, gu_s, xp, offsets, counts, act, E, 2 * I, H, 0, gu_q_b, gu_s_e, sb, -1, st, rmap, x_rows);
   launch_grouped<F>(d_q, d_s, act, offsets, counts, y, E, H, I, 1, d_q_b, d_s_e, sb, -1, st);
   return 0;
 }
@@ -930,6 +962,43 @@ API int dr_moe_prefill_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, cons
                                  int E, int H, int I, hipStream_t st) {
   return moe_prefill<FmtFP8<1>>(gu_w, gu_s, d_w, d_s, xp, offsets, counts, act, y, E, H, I, (size_t)2 * I * H,
                                 (size_t)(2 * I / 128) * (H / 128), (size_t)H * I, (size_t)(H / 128) * (I / 128), 2, st);
+}
+
+API int dr_moe_prefill_rows(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q, const uint16_t* d_sm,
+                            const uint16_t* x, int x_rows, const int* row_of_slot, const int* offsets,
+                            const int* counts, uint16_t* act, float* y, int E, int H, int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtQ4<ScaleF16>>(gu_q, gu_sm, d_q, d_sm, x, offsets, counts, act, y, E, H, I,
+                                      (size_t)2 * I * (H / 2), (size_t)2 * I * (H / 64) * 2, (size_t)H * (I / 2),
+                                      (size_t)H * (I / 64) * 2, 2, st, row_of_slot, x_rows);
+}
+
+API int dr_moe_prefill_rows_bf16s(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q, const uint16_t* d_sm,
+                                  const uint16_t* x, int x_rows, const int* row_of_slot, const int* offsets,
+                                  const int* counts, uint16_t* act, float* y, int E, int H, int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtQ4<ScaleBF16>>(gu_q, gu_sm, d_q, d_sm, x, offsets, counts, act, y, E, H, I,
+                                       (size_t)2 * I * (H / 2), (size_t)2 * I * (H / 64) * 2, (size_t)H * (I / 2),
+                                       (size_t)H * (I / 64) * 2, 2, st, row_of_slot, x_rows);
+}
+
+API int dr_moe_prefill_rows_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                                const uint16_t* x, int x_rows, const int* row_of_slot, const int* offsets,
+                                const int* counts, uint16_t* act, float* y, int E, int H, int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtFP8<0>>(gu_w, gu_s, d_w, d_s, x, offsets, counts, act, y, E, H, I, (size_t)2 * I * H,
+                                (size_t)(2 * I / 128) * (H / 128), (size_t)H * I, (size_t)(H / 128) * (I / 128), 4, st,
+                                row_of_slot, x_rows);
+}
+
+API int dr_moe_prefill_rows_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, const uint8_t* d_w,
+                                      const uint16_t* d_s, const uint16_t* x, int x_rows, const int* row_of_slot,
+                                      const int* offsets, const int* counts, uint16_t* act, float* y, int E, int H,
+                                      int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtFP8<1>>(gu_w, gu_s, d_w, d_s, x, offsets, counts, act, y, E, H, I, (size_t)2 * I * H,
+                                (size_t)(2 * I / 128) * (H / 128), (size_t)H * I, (size_t)(H / 128) * (I / 128), 2, st,
+                                row_of_slot, x_rows);
 }
 
 API int dr_moe_shared_prefill(const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q, const uint16_t* sd_s,

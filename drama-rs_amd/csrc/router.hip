@@ -14,15 +14,6 @@ namespace {
 
 constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
 
-// Pick k < topk <= 8 of the 32 group candidates, by rank (canon_merge_rank32): the candidate
-// of rank k is written to sel[k] and read back by lane k.  One wave, all lanes active.
-DEV int merge_picks(const uint64_t* cand, int* sel, int topk) {
-  const int lane = lane_id();
-  const int rk = canon_merge_rank32(cand);
-  if (lane < 32 && rk < topk) sel[rk] = canon_cand64_expert(cand[lane]);
-  return lane < topk ? sel[lane] : 0;
-}
-
 // Decode router: wave w of block b computes logit row RT_WPB b + w of the E + 1 rows.  All
 // loads of a wave (its weight row, x for the norm, x and nw for its dot lanes) are issued
 // before any arithmetic.  Logits are published with cache-bypassing (sc1) stores; after its

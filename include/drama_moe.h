@@ -182,6 +182,39 @@ int dr_moe_group(const int* idx, int n, int e, int* counts, int* offsets, int* s
 int dr_moe_gather_rows(const int* slot_of, int rows, int topk, const dr_bf16* x, dr_bf16* xp, int h,
                        dr_stream_t st);
 
+/* Prefill top-k and grouping in one launch: dr_moe_topk (same idx, wts and sgate bits) followed
+ * by dr_moe_group over the rows * topk pairs (same counts, offsets and slot_of), plus the inverse
+ * map row_of_slot[slot] = pair / topk, the token row each grouped slot takes its input from.
+ * counter (>= 4 bytes) must be 0 on entry and is 0 again on exit.  row_of_slot needs
+ * rows * topk + 16 entries (dr_moe_prefill_rows reads the map 16 entries at a time).
+ * Unsupported: rows * topk > 8192, e > 256, topk > 32, topk > e, stride < e + 1 -> -1. */
+int dr_moe_topk_group(const float* logits, int rows, int e, int topk, int stride, int* idx, float* wts,
+                      float* sgate, int* counts, int* offsets, int* slot_of, int* row_of_slot, uint32_t* counter,
+                      dr_stream_t st);
+
+/* dr_moe_group of rows * topk pairs plus row_of_slot as in dr_moe_topk_group (for a routing
+ * that does not come from dr_moe_topk_group).  Unsupported: rows * topk > 8192, e > 256 -> -1. */
+int dr_moe_group_rows(const int* idx, int rows, int topk, int e, int* counts, int* offsets, int* slot_of,
+                      int* row_of_slot, dr_stream_t st);
+
+/* dr_moe_prefill with the gate_up inputs read straight from the x_rows token rows of x through
+ * row_of_slot (from dr_moe_topk_group) instead of from a gathered xp: the same act and y bits as
+ * dr_moe_gather_rows followed by dr_moe_prefill, one launch and the xp copy fewer.  Formats as
+ * dr_moe_prefill, dr_moe_prefill_bf16s, dr_moe_prefill_fp8 and dr_moe_prefill_fp8_bf16s. */
+int dr_moe_prefill_rows(const uint8_t* gu_q, const dr_half* gu_sm, const uint8_t* d_q, const dr_half* d_sm,
+                        const dr_bf16* x, int x_rows, const int* row_of_slot, const int* offsets, const int* counts,
+                        dr_bf16* act, float* y, int e, int h, int i, dr_stream_t st);
+int dr_moe_prefill_rows_bf16s(const uint8_t* gu_q, const dr_bf16* gu_sm, const uint8_t* d_q, const dr_bf16* d_sm,
+                              const dr_bf16* x, int x_rows, const int* row_of_slot, const int* offsets,
+                              const int* counts, dr_bf16* act, float* y, int e, int h, int i, dr_stream_t st);
+int dr_moe_prefill_rows_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                            const dr_bf16* x, int x_rows, const int* row_of_slot, const int* offsets,
+                            const int* counts, dr_bf16* act, float* y, int e, int h, int i, dr_stream_t st);
+int dr_moe_prefill_rows_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, const uint8_t* d_w,
+                                  const dr_bf16* d_s, const dr_bf16* x, int x_rows, const int* row_of_slot,
+                                  const int* offsets, const int* counts, dr_bf16* act, float* y, int e, int h,
+                                  int i, dr_stream_t st);
+
 /* Prefill shared expert fused: act = bf16(silu(SG . hn) * (SU . hn)), out = SD . act (f32),
  * int8 weights dequantised in registers (replaces dr_dequant_q8 + dr_gemm + dr_swiglu_rows +
  * dr_dequant_q8 + dr_gemm of src/engine.rs:560-562).  act: scratch of rows * i bf16. */

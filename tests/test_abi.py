@@ -43,6 +43,13 @@ def test_error_strings_and_shape_errors_without_gpu():
     assert lib.raw("dr_moe_decode")(*([None] * 15), 4096, 512, 8, None, 0.0, None, 0, None) == -1
     assert lib.raw("dr_moe_prefill")(*([None] * 9), 256, 2048, 256, None) == -1
     assert lib.raw("dr_moe_group")(None, 9000, 256, None, None, None, None) == -1
+    # top-k with grouping: more than 8192 pairs, no counter, topk > e
+    assert lib.raw("dr_moe_topk_group")(None, 1025, 256, 8, 257, *([None] * 9)) == -1
+    assert lib.raw("dr_moe_topk_group")(None, 300, 256, 8, 257, *([None] * 9)) == -1
+    assert lib.raw("dr_moe_topk_group")(None, 300, 4, 8, 5, *([None] * 9)) == -1
+    assert lib.raw("dr_moe_group_rows")(None, 1025, 8, 256, None, None, None, None, None) == -1
+    assert lib.raw("dr_moe_prefill_rows_bf16s")(*([None] * 4), None, 300, None, None, None, None, None, 256, 4096,
+                                                512, None) == -1
     assert lib.raw("dr_gemv_q4_bf16s")(None, None, None, None, None, 10, 1000, None) == -1
 
 

@@ -193,6 +193,61 @@ def test_grouped_gemm(fmt, kind, skew):
         assert_close_with_flips(yp[sl], ryp[sl].astype(np.float64), Dm, af[sl], rf[sl], f"expert {e} end to end")
 
 
+@pytest.mark.parametrize("rows,E,topk", [(300, 256, 8), (1, 8, 8), (4, 256, 8), (1024, 256, 8), (37, 64, 12),
+                                         (5, 24, 2)])
+def test_topk_group_matches_oracle(rows, E, topk):
+    """dr_moe_topk_group: idx / wts / sgate bit for bit as the oracle's top-k, counts / offsets /
+    slot_of as its stable grouping, row_of_slot the inverse map, counter reset; logits with ties."""
+    import torch
+
+    rng = np.random.default_rng(rows * 7 + E + topk)
+    lg = rng.normal(0, 1, (rows, E + 1)).astype(np.float32)
+    lg[:, 1::5] = lg[:, 0:1]  # ties: equal logits across experts of a row
+    ri, rw, rs = O.moe_topk(lg.ravel(), rows, E, topk, E + 1)
+    rc, ro, rso = O.moe_group(ri, E)
+    n = rows * topk
+    dl, idx, wts, sg = dev(lg.ravel()), t_i32(n), torch.zeros(n, device="cuda"), torch.zeros(rows, device="cuda")
+    counts, offsets, slot_of, row_of_slot, counter = t_i32(E), t_i32(E), t_i32(n), t_i32(n + 16), t_i32(4)
+    D.lib().dr_moe_topk_group(D.ptr(dl), rows, E, topk, E + 1, D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(counts),
+                              D.ptr(offsets), D.ptr(slot_of), D.ptr(row_of_slot), D.ptr(counter), D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), ri)
+    np.testing.assert_array_equal(host(wts).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(host(sg).view(np.uint32), rs.view(np.uint32))
+    np.testing.assert_array_equal(host(counts), rc)
+    np.testing.assert_array_equal(host(offsets), ro)
+    np.testing.assert_array_equal(host(slot_of), rso)
+    np.testing.assert_array_equal(host(row_of_slot)[rso], np.arange(n) // topk)
+    assert int(host(counter)[0]) == 0, "counter not reset"
+
+
+@pytest.mark.parametrize("fmt,kind,skew", [("cfg", "q4", False), ("ref", "q4", False), ("cfg", "q4", True),
+                                           ("cfg", "fp8", False), ("ref", "fp8", False)])
+def test_prefill_rows_matches_gathered(fmt, kind, skew):
+    """dr_moe_prefill_rows*: the token rows read through row_of_slot give the same act and y bits
+    as the gathered xp through dr_moe_prefill*."""
+    import torch
+
+    E, rows, topk = 24, 96, 8
+    Lh = synth.make_layer(40 + (kind == "fp8"), E=E, fmt=fmt, kind=kind)
+    idx, counts, offsets, slot_of, x, xp = grouped_inputs(43, E, rows, topk, skew)
+    act_ref, y_ref = run_prefill(Lh, xp, offsets, counts, fmt, kind)
+    n = rows * topk
+    ros = np.zeros(n + 16, np.int32)
+    ros[slot_of] = np.arange(n) // topk
+    t = {k: dev(Lh[k]) for k in ("gu_q", "gu_s", "d_q", "d_s")}
+    dx, dros, doff, dcnt = dev(x), dev(ros), dev(offsets), dev(counts)
+    act = torch.zeros(n * I, dtype=torch.int16, device="cuda")
+    yp = torch.zeros(n * H, dtype=torch.float32, device="cuda")
+    name = {("q4", "ref"): "dr_moe_prefill_rows", ("q4", "cfg"): "dr_moe_prefill_rows_bf16s",
+            ("fp8", "ref"): "dr_moe_prefill_rows_fp8", ("fp8", "cfg"): "dr_moe_prefill_rows_fp8_bf16s"}[(kind, fmt)]
+    getattr(D.lib(), name)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(dx), rows,
+                           D.ptr(dros), D.ptr(doff), D.ptr(dcnt), D.ptr(act), D.ptr(yp), E, H, I, D.stream_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(act).view(np.uint16).reshape(n, I), act_ref)
+    np.testing.assert_array_equal(host(yp).reshape(n, H).view(np.uint32), y_ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("fmt", ["cfg", "ref"])
 @pytest.mark.parametrize("rows", [300, 33, 5, 1])
 def test_shared_prefill(fmt, rows):
@@ -241,9 +296,11 @@ def test_combine():
     assert_close(host(dx).reshape(rows, H), ref, rtol=1e-5, atol=1e-5, what="combine")
 
 
-@pytest.mark.parametrize("fmt", ["cfg", "ref"])
-def test_prefill_layer_chain(fmt):
-    """router GEMM -> top-k -> shared -> group -> gather -> grouped GEMM -> combine (E = 256)."""
+@pytest.mark.parametrize("fmt,path", [("cfg", "gather"), ("ref", "gather"), ("cfg", "rows"), ("ref", "rows")])
+def test_prefill_layer_chain(fmt, path):
+    """router GEMM -> top-k -> shared -> group -> gather -> grouped GEMM -> combine (E = 256);
+    path "rows": top-k with grouping in one launch, the grouped GEMM reading hn through the slot
+    map (dr_moe_topk_group + dr_moe_prefill_rows*)."""
     import torch
 
     E, rows, topk = 256, 300, 8
@@ -259,21 +316,31 @@ def test_prefill_layer_chain(fmt):
     h = np.zeros(1, np.uint64)
     L.dr_cublas_create(h.ctypes.data, sp)
     L.dr_gemm(int(h[0]), D.ptr(dhn), D.ptr(t["router"]), D.ptr(logits), rows, E + 1, H, 0.0)
-    L.dr_moe_topk(D.ptr(logits), rows, E, topk, E + 1, D.ptr(idx), D.ptr(wts), D.ptr(sg), sp)
+    counts, offsets, slot_of = t_i32(E), t_i32(E), t_i32(rows * topk)
+    row_of_slot, counter = t_i32(rows * topk + 16), t_i32(4)
+    if path == "rows":
+        L.dr_moe_topk_group(D.ptr(logits), rows, E, topk, E + 1, D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(counts),
+                            D.ptr(offsets), D.ptr(slot_of), D.ptr(row_of_slot), D.ptr(counter), sp)
+    else:
+        L.dr_moe_topk(D.ptr(logits), rows, E, topk, E + 1, D.ptr(idx), D.ptr(wts), D.ptr(sg), sp)
     sact = torch.zeros(rows * I, dtype=torch.int16, device="cuda")
     sh = torch.zeros(rows * H, device="cuda")
     shname = "dr_moe_shared_prefill_bf16s" if fmt == "cfg" else "dr_moe_shared_prefill"
     getattr(L, shname)(D.ptr(t["sgu_q"]), D.ptr(t["sgu_s"]), D.ptr(t["sd_q"]), D.ptr(t["sd_s"]), D.ptr(dhn), rows,
                        D.ptr(sact), D.ptr(sh), H, I, sp)
-    counts, offsets, slot_of = t_i32(E), t_i32(E), t_i32(rows * topk)
-    L.dr_moe_group(D.ptr(idx), rows * topk, E, D.ptr(counts), D.ptr(offsets), D.ptr(slot_of), sp)
-    xp = torch.zeros(rows * topk * H, dtype=torch.int16, device="cuda")
-    L.dr_moe_gather_rows(D.ptr(slot_of), rows, topk, D.ptr(dhn), D.ptr(xp), H, sp)
     act = torch.zeros(rows * topk * I, dtype=torch.int16, device="cuda")
     yp = torch.zeros(rows * topk * H, device="cuda")
-    pname = "dr_moe_prefill_bf16s" if fmt == "cfg" else "dr_moe_prefill"
-    getattr(L, pname)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(xp), D.ptr(offsets),
-                      D.ptr(counts), D.ptr(act), D.ptr(yp), E, H, I, sp)
+    if path == "rows":
+        pname = "dr_moe_prefill_rows_bf16s" if fmt == "cfg" else "dr_moe_prefill_rows"
+        getattr(L, pname)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(dhn), rows,
+                          D.ptr(row_of_slot), D.ptr(offsets), D.ptr(counts), D.ptr(act), D.ptr(yp), E, H, I, sp)
+    else:
+        L.dr_moe_group(D.ptr(idx), rows * topk, E, D.ptr(counts), D.ptr(offsets), D.ptr(slot_of), sp)
+        xp = torch.zeros(rows * topk * H, dtype=torch.int16, device="cuda")
+        L.dr_moe_gather_rows(D.ptr(slot_of), rows, topk, D.ptr(dhn), D.ptr(xp), H, sp)
+        pname = "dr_moe_prefill_bf16s" if fmt == "cfg" else "dr_moe_prefill"
+        getattr(L, pname)(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), D.ptr(t["d_q"]), D.ptr(t["d_s"]), D.ptr(xp),
+                          D.ptr(offsets), D.ptr(counts), D.ptr(act), D.ptr(yp), E, H, I, sp)
     L.dr_moe_combine(D.ptr(dx), D.ptr(yp), D.ptr(slot_of), D.ptr(wts), D.ptr(sg), D.ptr(sh), rows, topk, H, sp)
     torch.cuda.synchronize()
     # routing: bit-exact against the oracle's canonical GEMM + softmax/top-k
@@ -285,6 +352,10 @@ def test_prefill_layer_chain(fmt):
     rc, ro, rso = O.moe_group(ri, E)
     np.testing.assert_array_equal(host(counts), rc)
     np.testing.assert_array_equal(host(slot_of), rso)
+    if path == "rows":
+        np.testing.assert_array_equal(host(offsets), ro)
+        np.testing.assert_array_equal(host(row_of_slot)[rso], np.arange(rows * topk) // topk)
+        assert int(host(counter)[0]) == 0, "counter not reset"
     ref = O.moe_prefill_layer(Lh, hn, rows, ri, rw, rs, x0, H, I, topk).astype(np.float64)
     # intermediates of the oracle, to bound the effect of bf16 act rounding flips
     n = rows * topk

@@ -366,6 +366,23 @@ def config5_fp8(lib, st, iters=100, copies=4):
                                note="4 rows via the small-batch decode path (dr_router_topk_rows + "
                                     "dr_moe_decode_rows_fp8_bf16s, 3 launches); bytes = router + distinct "
                                     "experts + shared + vectors; us_graph: replayed from a HIP graph")
+    # the same with the router in the gate_up launch (2 launches)
+    c4, tags4 = z(4, torch.int32), z(384, torch.int64)
+
+    def b4f(i):
+        Lc = Ls[i % copies]
+        lib.dr_moe_decode_rows_routed_fp8_bf16s(P(Lc["router"]), P(Lc["nw"]), 1e-6, E, P(Lc["gu_q"]), P(Lc["gu_s"]),
+                                                P(Lc["d_q"]), P(Lc["d_s"]), P(Lc["sgu_q"]), P(Lc["sgu_s"]),
+                                                P(Lc["sd_q"]), P(Lc["sd_s"]), P(x4), P(lg4), P(idx4), P(wts4), P(sg4),
+                                                P(c4), P(tags4), P(x4), P(act4), P(x4), None, 4, H, I, TOPK, sp)
+
+    ms4f = timed(b4f, iters, st)
+    ms4fg = timed_graph(b4f, iters, st, copies)
+    if lib.dr_last_error() != 0:
+        raise RuntimeError("dr_moe_decode_rows_routed_fp8_bf16s reported an error")
+    out["decode_batch4_routed"] = rec(ms4f * 1000, nb4r, experts_hit=hit4, us_graph=round(ms4fg * 1000, 2),
+                                      note="4 rows, router + top-k in the gate_up launch, then down "
+                                           "(dr_moe_decode_rows_routed_fp8_bf16s, 2 launches); bytes as decode_batch4")
     del L, Ls, routers
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections

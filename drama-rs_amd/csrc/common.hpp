@@ -18,8 +18,8 @@ constexpr int WAVE = 64;
 // whose bounded wait gave up (system-scope store) and read by the host without synchronising
 // (dr_last_error, dr_stream_sync, the launchers).  err_word() returns its device address,
 // nullptr if it could not be set up; err_pending() the current code (0 = none).
-// Codes (the header's DR_ERR_STEP_TIMEOUT / DR_ERR_PREFILL_WAIT).
-constexpr uint32_t kErrStepTimeout = 9001, kErrPrefillWait = 9002;
+// Codes (the header's DR_ERR_STEP_TIMEOUT / DR_ERR_PREFILL_WAIT / DR_ERR_ROUTE_WAIT).
+constexpr uint32_t kErrStepTimeout = 9001, kErrPrefillWait = 9002, kErrRouteWait = 9003;
 uint32_t* err_word();
 uint32_t err_pending();
 

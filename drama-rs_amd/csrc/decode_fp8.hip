@@ -10,7 +10,7 @@
 // benchmark configuration); every 16-element lane chunk lies inside one block.
 #include <type_traits>
 
-#include "common.hpp"
+#include "router_rows.hpp"
 
 using namespace drm;
 
@@ -43,25 +43,26 @@ DEV void unpack16(const float4* xs, int lane, float (&xa)[16], float (&xb)[16], 
 // and loading unit p + D once unit p is computed.  The shared-expert blocks that follow (PPWS
 // pairs per wave, all loaded at once) serve all B rows with one read of their weights.  x
 // (and the norm weight) are requested before the weights, so the staging overlaps the fetch.
-template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B>
-__global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 1)))
-    k_moe_gate_up_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
-                      const uint16_t* __restrict__ shs, const float* x, const int* __restrict__ idx,
-                      float* __restrict__ act, const float* nw, float eps) {
+// Block blk of the gate_up grid (shared blocks first); the picks come from Picks: wait() is
+// called by every thread of a routed block once its x is requested, get(i) returns pick i.
+template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B, class Picks>
+DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* __restrict__ S,
+                           const int8_t* __restrict__ shq, const uint16_t* __restrict__ shs, const float* x,
+                           const Picks& picks, float* __restrict__ act, const float* nw, float eps, float4* xs) {
   constexpr int H = H8, I = I8, NT = WPB * 64, NW = NBR * WPB, PPW = B * TOPK8 * I / NW;
   static_assert(PPW * NW == B * TOPK8 * I && D <= PPW, "units split evenly over the routed waves");
   constexpr int NBS = I / (WPB * PPWS);  // shared-expert blocks, dispatched first
   const int lane = lane_id(), wave = wave_id();
-  __shared__ float4 xs[B * H / 4];
-  if ((int)blockIdx.x >= NBS) {
-    const int g = (blockIdx.x - NBS) * WPB + wave;
+  if (blk >= NBS) {
+    const int g = (blk - NBS) * WPB + wave;
     XStage<H, NT, B, SlotQ8H> xst;
     xst.load(x, nw);
+    picks.wait();
     uint4 g0[D], g1[D], u0[D], u1[D];
     uint32_t sr[D][4];
     auto issue = [&](int p, int d) {
       const int u = g + NW * p, b = u / (TOPK8 * I), k = (u / I) % TOPK8, j = u % I;
-      const size_t e = (size_t)idx[b * TOPK8 + k];
+      const size_t e = (size_t)picks.get(b * TOPK8 + k);
       const uint8_t* rg = W + (e * (2 * I) + j) * H + lane * 16;
       const uint8_t* ru = rg + (size_t)I * H;
       g0[d] = ld16(rg), g1[d] = ld16(rg + 1024), u0[d] = ld16(ru), u1[d] = ld16(ru + 1024);
@@ -90,7 +91,7 @@ __global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(W
       if (lane == 0) act[(size_t)b * (TOPK8 + 1) * I + k * I + j] = silu(gv) * uv;
     }
   } else {
-    const int j0 = (blockIdx.x * WPB + wave) * PPWS;
+    const int j0 = (blk * WPB + wave) * PPWS;
     XStage<H, NT, B, SlotQ8H> xst;
     xst.load(x, nw);
     uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
@@ -126,10 +127,194 @@ __global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(W
   }
 }
 
-// down of decode row blockIdx.y: wave w of block b owns output rows n0 .. n0 + RPW - 1 and
-// gathers, per row, the 8 routed expert rows of 512 bytes (load i: experts 2 i on lanes 0-31,
-// 2 i + 1 on lanes 32-63) and 8 bytes of the int8 shared row per lane; the row's activations
-// are staged in LDS.
+struct PicksGlobal {
+  const int* idx;
+  DEV void wait() const {}
+  DEV int get(int i) const { return idx[i]; }
+};
+
+template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B>
+__global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 1)))
+    k_moe_gate_up_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
+                      const uint16_t* __restrict__ shs, const float* x, const int* __restrict__ idx,
+                      float* __restrict__ act, const float* nw, float eps) {
+  __shared__ float4 xs[B * H8 / 4];
+  gate_up_fp8_block<SF, SH, WPB, NBR, D, PPWS, B>(blockIdx.x, W, S, shq, shs, x, PicksGlobal{idx}, act, nw, eps, xs);
+}
+
+// The picks of the fused router + gate_up launch: wave 0 of the block polls the B * 8 tagged
+// words (tag << 32) | expert that the router's last block publishes, until every tag is the
+// launch's (bounded: on time-out DR_ERR_ROUTE_WAIT is raised and expert 0 is used), and leaves
+// the experts in LDS for the block.
+template <int B>
+struct PicksTagged {
+  const uint64_t* tags;
+  uint32_t tag;
+  int* s_idx;
+  uint32_t* err;
+  DEV void wait() const {
+    constexpr int n = B * TOPK8;
+    if (wave_id() == 0) {
+      const int lane = lane_id();
+      uint64_t v = (uint64_t)tag << 32;
+      for (int it = 0;; ++it) {
+        if (lane < n) v = __hip_atomic_load(tags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__ballot((uint32_t)(v >> 32) != tag) == 0) break;
+        if (it == (1 << 20)) {
+          if (lane == 0) raise_err(err, kErrRouteWait);
+          v = (uint64_t)tag << 32;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (lane < n) s_idx[lane] = (int)(uint32_t)v;
+    }
+    __syncthreads();
+  }
+  DEV int get(int i) const { return s_idx[i]; }
+};
+
+// The launch's finished-block count without one hot address (hundreds of same-address
+// atomics serialise): block c of nb adds itself to group counter c % RC_G, each on its own
+// 128-byte line in the tags buffer after the picks, and the block that fills its group adds
+// one to a top counter; the block that fills the top is the launch's last.  Counters start at
+// zero and the last block resets them.
+constexpr int RC_G = 16, RC_DONE = 128, RC_WORDS = RC_DONE + 16 * RC_G;
+static_assert(RC_WORDS == 384, "the tags buffer size the header states");
+static_assert(RC_DONE >= 4 * (2 * TOPK8 + 1), "picks before the counters");
+DEV uint32_t* rc_ctr(uint64_t* tags, int base, int g) { return reinterpret_cast<uint32_t*>(tags + base + 16 * g); }
+DEV uint32_t rc_n(int nb, int g) { return (uint32_t)(nb / RC_G + (g < nb % RC_G ? 1 : 0)); }
+// one thread per block; true for the block that completes the count
+DEV bool rc_add(uint64_t* tags, int base, uint32_t* top, int c, int nb) {
+  const int g = c % RC_G;
+  if (__hip_atomic_fetch_add(rc_ctr(tags, base, g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != rc_n(nb, g) - 1u)
+    return false;
+  return __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)RC_G - 1u;
+}
+// one wave
+DEV void rc_reset(uint64_t* tags, int base) {
+  if (lane_id() < RC_G) __hip_atomic_store(rc_ctr(tags, base, lane_id()), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// End of a launch, wave 0 of every block: the block that completes the done count resets the
+// done counters and counter[2] and advances the tag in counter[1].  Every block read the tag
+// at its start, before it counted.
+DEV void launch_done(uint64_t* tags, uint32_t* counter, int blk, int nb, uint32_t tag) {
+  const int lane = lane_id();
+  bool last = false;
+  if (lane == 0) last = rc_add(tags, RC_DONE, counter + 2, blk, nb);
+  if (!__ballot(last)) return;
+  rc_reset(tags, RC_DONE);
+  if (lane == 0) {
+    __hip_atomic_store(counter + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(counter + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Router, top-k and gate_up of B decode rows in one launch.  Blocks [0, NRB) run the router
+// of router_rows.hpp (its last block publishes the picks as tagged words), then the gate_up
+// grid of k_moe_gate_up_fp8 follows: its shared-expert blocks need no picks, its routed blocks
+// request their x and then wait for the picks.  A block waits only for blocks of lower index,
+// which are dispatched first, so the launch needs no co-residency.  counter: [0] the router's
+// arrivals (reset by its last block), [1] the tag of the previous launch, [2] the top of the
+// finished-block count (launch_done), whose last block advances [1], so every launch tags its
+// picks afresh.
+template <int SF, class SH, int NBR, int D, int PPWS, int B>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+    k_moe_route_gate_up_fp8(const uint16_t* __restrict__ RW, float* __restrict__ logits, int E,
+                            int* __restrict__ idx, float* __restrict__ wts, float* __restrict__ sgate,
+                            uint32_t* __restrict__ counter, uint64_t* __restrict__ tags, uint32_t* err,
+                            const uint8_t* __restrict__ W, const void* __restrict__ S,
+                            const int8_t* __restrict__ shq, const uint16_t* __restrict__ shs, const float* x,
+                            float* __restrict__ act, const float* nw, float eps) {
+  __shared__ float4 xs[B * H8 / 4];
+  __shared__ int s_idx[B * TOPK8];
+  __shared__ uint32_t s_tag;
+  if (threadIdx.x == 0) s_tag = __hip_atomic_load(counter + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  __syncthreads();
+  const uint32_t tag = s_tag;
+  const int nrb = (E + RT_WPB) / RT_WPB;
+  if ((int)blockIdx.x < nrb) {
+    router_rows_block<B>(blockIdx.x, nrb, RW, x, nw, eps, logits, E, TOPK8, idx, wts, sgate, counter, tags, tag,
+                         reinterpret_cast<float4(*)[H8 / 4]>(xs));
+  } else {
+    gate_up_fp8_block<SF, SH, 8, NBR, D, PPWS, B>(blockIdx.x - nrb, W, S, shq, shs, x,
+                                                  PicksTagged<B>{tags, tag, s_idx, err}, act, nw, eps, xs);
+  }
+  if (wave_id() == 0) launch_done(tags, counter, blockIdx.x, gridDim.x, tag);
+}
+
+// The down weights of output rows n0 .. n0 + RPW - 1: per row the 8 routed expert rows of
+// 512 bytes (load i: experts 2 i on lanes 0-31, 2 i + 1 on lanes 32-63, e[i] per lane) and 8
+// bytes of the int8 shared row per lane.
+template <int SF, class SH, int RPW>
+struct DownFP8 {
+  uint4 q[RPW][4];
+  uint32_t sc[RPW][4];
+  uint2 qs[RPW];
+  uint32_t ssr[RPW];
+  DEV void issue(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
+                 const uint16_t* __restrict__ shs, const size_t (&e)[4], int n0) {
+    constexpr int H = H8, I = I8;
+    const int lane = lane_id(), cc = lane & 31;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const size_t n = (size_t)(n0 + r);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q[r][i] = ld16(W + (e[i] * H + n) * I + cc * 16);
+        sc[r][i] = blk_raw<SF>(S, (e[i] * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
+      }
+      qs[r] = ld8(shq + n * I + lane * 8);
+      ssr[r] = SH::raw(shs, n, lane * 8, I);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // as: the row's activations staged by stage_slot (routed part in lane slices, shared part at
+  // 1024); w[i] the pick weight of e[i]; y[n] = res[n] + routed + sigmoid(gate) * shared
+  DEV void finish(const float4* as, const float (&w)[4], float sgv, const float* res, float* y, uint16_t* yb,
+                  size_t nb) const {
+    const int lane = lane_id();
+    float xa[4][16], xc[8], sumc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 v = as[256 * i + t * 64 + lane];
+        xa[i][4 * t] = v.x, xa[i][4 * t + 1] = v.y, xa[i][4 * t + 2] = v.z, xa[i][4 * t + 3] = v.w;
+      }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float4 v = as[1024 + t * 64 + lane];
+      xc[4 * t] = v.x, xc[4 * t + 1] = v.y, xc[4 * t + 2] = v.z, xc[4 * t + 3] = v.w;
+      sumc += (v.x + v.y) + (v.z + v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc += w[i] * blk_cvt<SF>(sc[r][i]) * dot16_fp8(q[r][i], xa[i], 0.f);
+      float dc = dot4_u8b(qs[r].x, xc, 0.f);
+      dc = dot4_u8b(qs[r].y, xc + 4, dc);
+      acc += sgv * SH::cvt(ssr[r]) * (dc - 128.f * sumc);
+      acc = wave_sum(acc);
+      const size_t n = nb + r;
+      if (lane == 0) {
+        const float out = res[n] + acc;
+        y[n] = out;
+        if (yb) yb[n] = to_bf16(out);
+      }
+    }
+  }
+};
+// LDS slot of activation float4 f of a row ((TOPK8 + 1) * I / 4 of them): the routed part in
+// the lane slices DownFP8 reads (load i = act[1024 i + 16 l .. + 16) -> 4 float4 per part of
+// 256), the shared part's 8 floats per lane at 1024 + t * 64 + l
+DEV int down_slot(int f) {
+  return f < 1024 ? (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2) : 1024 + ((f - 1024) & 1) * 64 + ((f - 1024) >> 1);
+}
+
+// down of decode row blockIdx.y: wave w of block b owns output rows n0 .. n0 + RPW - 1
+// (DownFP8); the row's activations are requested first and staged in LDS.
 template <int SF, class SH, int WPB, int RPW>
 __global__ void __launch_bounds__(WPB * 64)
     k_moe_down_fp8(const uint8_t* __restrict__ W, const void* __restrict__ S, const int8_t* __restrict__ shq,
@@ -139,7 +324,7 @@ __global__ void __launch_bounds__(WPB * 64)
   constexpr int H = H8, I = I8, AW = (TOPK8 + 1) * I / 4, NT = WPB * 64;
   __shared__ float4 as[AW];
   const int lane = lane_id(), wave = wave_id();
-  const int half = lane >> 5, cc = lane & 31, b = blockIdx.y;
+  const int half = lane >> 5, b = blockIdx.y;
   const int n0 = (blockIdx.x * WPB + wave) * RPW;
   act += (size_t)b * (TOPK8 + 1) * I, idx += b * TOPK8, wts += b * TOPK8;
   // pick indices with scalar loads, then the activations (requested before the weights, so
@@ -161,63 +346,13 @@ __global__ void __launch_bounds__(WPB * 64)
   for (int t = 0; t < NA; ++t) av[t] = ldf4(a4 + threadIdx.x + NT * t);
   av[NA] = ldf4(a4 + 1024 + (threadIdx.x & 127));
   issue_fence();
-  uint4 q[RPW][4];
-  uint32_t sc[RPW][4];
-  uint2 qs[RPW];
-  uint32_t ssr[RPW];
+  DownFP8<SF, SH, RPW> dn;
+  dn.issue(W, S, shq, shs, e, n0);
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const size_t n = (size_t)(n0 + r);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      q[r][i] = ld16(W + (e[i] * H + n) * I + cc * 16);
-      sc[r][i] = blk_raw<SF>(S, (e[i] * (H / 128) + (n >> 7)) * (I / 128) + (cc >> 3));
-    }
-    qs[r] = ld8(shq + n * I + lane * 8);
-    ssr[r] = SH::raw(shs, n, lane * 8, I);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // routed act: lane slice of load i = act[1024 i + 16 l .. + 16) -> 4 float4 per part of 256
-#pragma unroll
-  for (int t = 0; t < NA; ++t) {
-    const int f = threadIdx.x + NT * t;
-    as[(f & ~255) + (f & 3) * 64 + ((f & 255) >> 2)] = av[t];
-  }
-  if ((int)threadIdx.x < 128) {
-    const int f = threadIdx.x;
-    as[1024 + (f & 1) * 64 + (f >> 1)] = av[NA];
-  }
+  for (int t = 0; t < NA; ++t) as[down_slot(threadIdx.x + NT * t)] = av[t];
+  if ((int)threadIdx.x < 128) as[down_slot(1024 + threadIdx.x)] = av[NA];
   __syncthreads();
-  float xa[4][16], xc[8], sumc = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float4 v = as[256 * i + t * 64 + lane];
-      xa[i][4 * t] = v.x, xa[i][4 * t + 1] = v.y, xa[i][4 * t + 2] = v.z, xa[i][4 * t + 3] = v.w;
-    }
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float4 v = as[1024 + t * 64 + lane];
-    xc[4 * t] = v.x, xc[4 * t + 1] = v.y, xc[4 * t + 2] = v.z, xc[4 * t + 3] = v.w;
-    sumc += (v.x + v.y) + (v.z + v.w);
-  }
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc += w[i] * blk_cvt<SF>(sc[r][i]) * dot16_fp8(q[r][i], xa[i], 0.f);
-    float dc = dot4_u8b(qs[r].x, xc, 0.f);
-    dc = dot4_u8b(qs[r].y, xc + 4, dc);
-    acc += sgv * SH::cvt(ssr[r]) * (dc - 128.f * sumc);
-    acc = wave_sum(acc);
-    const size_t n = (size_t)b * H + n0 + r;
-    if (lane == 0) {
-      const float out = res[n] + acc;
-      y[n] = out;
-      if (yb) yb[n] = to_bf16(out);
-    }
-  }
+  dn.finish(as, w, sgv, res, y, yb, (size_t)b * H + n0);
   warm_range(pf, pf_bytes);
 }
 
@@ -266,6 +401,42 @@ int launch_decode_fp8(const uint8_t* gu_w, const void* gu_s, const uint8_t* d_w,
   return 0;
 }
 
+// The small-batch path with the router in the gate_up launch, rows in chunks of four (each
+// chunk's logits and picks at its row offset; every launch tags its picks afresh in the same
+// tags words), then down.
+template <int SF, class SH>
+int launch_decode_routed_fp8(const uint16_t* rw, float* logits, int E, int* idx, float* wts, float* sgate,
+                             uint32_t* counter, uint64_t* tags, const uint8_t* gu_w, const void* gu_s,
+                             const uint8_t* d_w, const void* d_s, const int8_t* sgu_q, const uint16_t* sgu_s,
+                             const int8_t* sd_q, const uint16_t* sd_s, const float* x, const float* res, float* act,
+                             float* y, uint16_t* yb, int rows, int H, int I, int topk, const float* nw, float eps,
+                             hipStream_t st) {
+  if (H != H8 || I != I8 || topk != TOPK8 || rows < 1 || rows > 64 || E < TOPK8 || E > 256) return -1;
+  if (!rw || !logits || !idx || !wts || !sgate || !counter || !tags) return -1;
+  uint32_t* err = err_word();
+  constexpr int NBR = 512, PPWS = 2, NBS = I8 / (8 * PPWS);
+  const int nrb = (E + RT_WPB) / RT_WPB;
+  for (int r0 = 0; r0 < rows; r0 += 4) {
+    const int b = rows - r0 < 4 ? rows - r0 : 4;
+    const size_t xo = (size_t)r0 * H, ko = (size_t)r0 * topk, ao = (size_t)r0 * (topk + 1) * I;
+    float* lg = logits + (size_t)r0 * (E + 1);
+    auto go = [&](auto kb) {
+      constexpr int KB = decltype(kb)::value, D = KB < 2 ? KB : 2, DW = KB == 1 ? 4 : 8, DR = 2;
+      hipLaunchKernelGGL((k_moe_route_gate_up_fp8<SF, SH, NBR, D, PPWS, KB>), dim3(nrb + NBS + NBR), dim3(512), 0, st,
+                         rw, lg, E, idx + ko, wts + ko, sgate + r0, counter, tags, err, gu_w, gu_s, sgu_q, sgu_s,
+                         x + xo, act + ao, nw, eps);
+      hipLaunchKernelGGL((k_moe_down_fp8<SF, SH, DW, DR>), dim3(H8 / (DW * DR), KB), dim3(DW * 64), 0, st, d_w, d_s,
+                         sd_q, sd_s, act + ao, idx + ko, wts + ko, sgate + r0, res + xo, y + xo,
+                         yb ? yb + xo : nullptr, nullptr, (size_t)0);
+    };
+    if (b == 1) go(std::integral_constant<int, 1>{});
+    else if (b == 2) go(std::integral_constant<int, 2>{});
+    else if (b == 3) go(std::integral_constant<int, 3>{});
+    else go(std::integral_constant<int, 4>{});
+  }
+  return 0;
+}
+
 }  // namespace
 
 API int dr_moe_decode_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
@@ -304,3 +475,27 @@ API int dr_moe_decode_rows_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, 
   return launch_decode_fp8<1, Q8RowBF16>(gu_w, gu_s, d_w, d_s, sgu_q, sgu_s, sd_q, sd_s, x, idx, wts, sgate, res, act,
                                          y, yb, H, I, topk, nw, eps, nullptr, 0, st, rows);
 }
+
+API int dr_moe_decode_rows_routed_fp8(const uint16_t* router_w, const float* nw, float eps, int E,
+                                      const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                                      const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_q,
+                                      const uint16_t* sd_s, const float* x, float* logits, int* idx, float* wts,
+                                      float* sgate, uint32_t* counter, uint64_t* tags, const float* res, float* act,
+                                      float* y, int rows, int H, int I, int topk, hipStream_t st) {
+  return launch_decode_routed_fp8<0, Q8G128F16>(router_w, logits, E, idx, wts, sgate, counter, tags, gu_w, gu_s, d_w,
+                                                d_s, sgu_q, sgu_s, sd_q, sd_s, x, res, act, y, nullptr, rows, H, I,
+                                                topk, nw, eps, st);
+}
+
+API int dr_moe_decode_rows_routed_fp8_bf16s(const uint16_t* router_w, const float* nw, float eps, int E,
+                                            const uint8_t* gu_w, const uint16_t* gu_s, const uint8_t* d_w,
+                                            const uint16_t* d_s, const int8_t* sgu_q, const uint16_t* sgu_s,
+                                            const int8_t* sd_q, const uint16_t* sd_s, const float* x, float* logits,
+                                            int* idx, float* wts, float* sgate, uint32_t* counter, uint64_t* tags,
+                                            const float* res, float* act, float* y, uint16_t* yb, int rows, int H,
+                                            int I, int topk, hipStream_t st) {
+  return launch_decode_routed_fp8<1, Q8RowBF16>(router_w, logits, E, idx, wts, sgate, counter, tags, gu_w, gu_s, d_w,
+                                                d_s, sgu_q, sgu_s, sd_q, sd_s, x, res, act, y, yb, rows, H, I, topk,
+                                                nw, eps, st);
+}
+

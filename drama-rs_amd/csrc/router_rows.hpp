@@ -1,0 +1,161 @@
+// Decode router for B rows (B <= 8) as one block's work: shared by dr_router_topk_rows (a
+// launch of router blocks only) and the fused small-batch FP8 kernel (router blocks ahead of
+// the gate_up blocks in one launch).  Reference semantics: kernels/drama.cu:317-461 per row.
+//
+// Block blk of nblk: wave w computes logit row RT_WPB blk + w for every row, its weight row
+// loaded once.  The rows of x are staged in LDS, wave r < B computes row r's canonical RMSNorm
+// scale, and the block normalises the staged rows in place (canon_norm4 is elementwise, so the
+// values equal those k_router_topk forms in registers).  Every logit has the canonical order
+// of canon.hpp, so each row's logits, picks and weights equal those of dr_router_topk on that
+// row.  Logits are published with cache-bypassing (sc1) stores; each block counts itself in
+// once its stores completed, and the last block loads the logits of all rows at once and
+// spreads the per-row work over its waves: for topk <= 8 the 4 B group selections and B
+// softmax denominators, then one rank merge per row; for topk > 8 one wave per row.  It
+// writes idx, wts and sgate, and (tags != nullptr) also publishes them as tagged words
+// (tag << 32) | value bits with cache-bypassing stores, for blocks of the same launch to poll:
+// row r's experts at tags[r topk ..], its weights at tags[(B + r) topk ..], its shared-expert
+// gate logit at tags[2 B topk + r].
+// It resets the counter.  Every thread returns normally (no early exit), so callers may add
+// work after it.
+#pragma once
+#include "canon.hpp"
+
+namespace drm {
+
+constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
+
+template <int B>
+DEV void router_rows_block(int blk, int nblk, const uint16_t* __restrict__ W, const float* __restrict__ x,
+                           const float* __restrict__ nw, float eps, float* __restrict__ logits, int E, int topk,
+                           int* __restrict__ idx, float* __restrict__ wts, float* __restrict__ sgate,
+                           uint32_t* __restrict__ counter, uint64_t* __restrict__ tags, uint32_t tag,
+                           float4 (*xs)[2048 / 4]) {
+#pragma clang fp contract(off)
+  constexpr int K = 2048, NCH = K / 8 / WAVE, NRM = K / 4 / WAVE, NT = RT_WPB * 64;
+  __shared__ float s_inv[B];
+  __shared__ int s_last;
+  const int lane = lane_id(), wave = wave_id();
+  const int row = blk * RT_WPB + wave;
+  uint4 w[NCH];
+  if (row <= E) {
+    const uint16_t* wr = W + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) w[j] = ld16(wr + (size_t)(lane + WAVE * j) * 8);
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* n4 = reinterpret_cast<const float4*>(nw);
+  float4 nv[K / 4 / NT];
+  if (nw) {
+#pragma unroll
+    for (int i = 0; i < K / 4 / NT; ++i) nv[i] = n4[threadIdx.x + NT * i];
+  }
+#pragma unroll
+  for (int i = threadIdx.x; i < B * K / 4; i += NT) xs[i / (K / 4)][i % (K / 4)] = x4[i];
+  __syncthreads();
+  if (nw) {
+    if (wave < B) {
+      float4 xr[NRM];
+#pragma unroll
+      for (int j = 0; j < NRM; ++j) xr[j] = xs[wave][lane + WAVE * j];
+      const float inv = canon_rms_inv_regs<NRM>(xr, eps);
+      if (lane == 0) s_inv[wave] = inv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < B; ++r)
+#pragma unroll
+      for (int i = 0; i < K / 4 / NT; ++i) {
+        const int c = threadIdx.x + NT * i;
+        xs[r][c] = canon_norm4(xs[r][c], s_inv[r], nv[i]);
+      }
+    __syncthreads();
+  }
+  if (row <= E) {
+#pragma unroll
+    for (int r = 0; r < B; ++r) {
+      float4 xa[NCH], xb[NCH];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int c = lane + WAVE * j;
+        xa[j] = xs[r][2 * c], xb[j] = xs[r][2 * c + 1];
+      }
+      const float acc = canon_row_dot<NCH>(w, xa, xb);
+      if (lane == 0) __hip_atomic_store(logits + (size_t)r * (E + 1) + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)nblk - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __shared__ float lg[B][257];
+  __shared__ uint64_t s_cand[B][32];
+  __shared__ int s_sel[B][8];
+  __shared__ float s_mz[B][2];
+  {
+    // every row's logits requested at once (one round trip), then stored
+    constexpr int NL = (B * 257 + NT - 1) / NT;
+    float v[NL];
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = threadIdx.x + NT * t;
+      v[t] = i < B * (E + 1) ? __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int i = threadIdx.x + NT * t;
+      if (i < B * (E + 1)) {
+        const int r = i / (E + 1);
+        lg[r][i - r * (E + 1)] = v[t];
+      }
+    }
+  }
+  __syncthreads();
+  auto publish = [&](int r, int id, float wt) {
+    if (lane < topk) {
+      idx[r * topk + lane] = id, wts[r * topk + lane] = wt;
+      if (tags) {
+        __hip_atomic_store(tags + r * topk + lane, ((uint64_t)tag << 32) | (uint32_t)id, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(tags + (B + r) * topk + lane, ((uint64_t)tag << 32) | __float_as_uint(wt),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  };
+  if (topk <= 8) {
+    for (int t = wave; t < 5 * B; t += RT_WPB) {
+      const int r = t / 5, sub = t - 5 * r;
+      if (sub < 4) {
+        int ck, ce;
+        canon_select_group8(lg[r], E, sub, &ck, &ce);
+        if (lane < 8) s_cand[r][sub * 8 + lane] = canon_cand64(ck, ce);
+      } else {
+        float m;
+        const float z = canon_softmax_z(lg[r], E, &m);
+        if (lane == 0) s_mz[r][0] = m, s_mz[r][1] = z;
+      }
+    }
+    __syncthreads();
+    for (int r = wave; r < B; r += RT_WPB) {
+      const int id = merge_picks(s_cand[r], s_sel[r], topk);
+      publish(r, id, canon_topk_weight(lg[r][lane < topk ? id : 0], s_mz[r][0], s_mz[r][1], topk));
+    }
+  } else {
+    for (int r = wave; r < B; r += RT_WPB) {
+      int my_idx;
+      float my_w;
+      canon_softmax_topk(lg[r], E, topk, &my_idx, &my_w);
+      publish(r, my_idx, my_w);
+    }
+  }
+  if ((int)threadIdx.x < B) {
+    sgate[threadIdx.x] = lg[threadIdx.x][E];
+    if (tags)
+      __hip_atomic_store(tags + 2 * B * topk + threadIdx.x, ((uint64_t)tag << 32) | __float_as_uint(lg[threadIdx.x][E]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace drm

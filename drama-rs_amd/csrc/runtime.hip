@@ -45,6 +45,7 @@ API const char* dr_error_string(int e) {
   if (e == (int)kErrStepTimeout)
     return "fused decode step gave up waiting for its workgroups (not co-resident: another kernel held CUs)";
   if (e == (int)kErrPrefillWait) return "prefill grouped GEMM gave up waiting for an LDS hand-off";
+  if (e == (int)kErrRouteWait) return "fused small-batch decode gave up waiting for the router's picks";
   return hipGetErrorString((hipError_t)e);
 }
 // The runtime's last launch error first; then a pending library error, which this call clears.

@@ -60,7 +60,9 @@ constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrea
 // (one fp32 per word).
 constexpr int LL_LOG = 0, LL_ACT = 264, LL_X = LL_ACT + ST_TOPK * ST_I + ST_I, LL_WORDS = LL_X + ST_H;
 static_assert(LL_WORDS == DR_STEP_LL_WORDS, "slot layout");
-static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT, "error codes");
+static_assert(kErrStepTimeout == DR_ERR_STEP_TIMEOUT && kErrPrefillWait == DR_ERR_PREFILL_WAIT &&
+                  kErrRouteWait == DR_ERR_ROUTE_WAIT,
+              "error codes");
 
 // Phase timestamps for development builds (-DST_TRACE): thread 0 of each block stores the
 // 100 MHz clock at points 0..7, 9 and 11..14 of each layer (poll rounds at 8, 10 and 15) into

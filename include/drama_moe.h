@@ -38,6 +38,7 @@ extern "C" {
  * launchers refuse to start while it is set, and dr_last_error returns and clears it. */
 #define DR_ERR_STEP_TIMEOUT 9001 /* fused step: workgroups not co-resident within the wait limit */
 #define DR_ERR_PREFILL_WAIT 9002 /* prefill grouped GEMM: an LDS hand-off between waves timed out */
+#define DR_ERR_ROUTE_WAIT 9003 /* fused small-batch router + experts: the picks did not arrive in time */
 
 typedef void* dr_stream_t;     /* hipStream_t */
 typedef void* dr_graph_exec_t; /* hipGraphExec_t */
@@ -276,6 +277,32 @@ int dr_moe_decode_rows_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, const
                                  const float* x, const int* idx, const float* wts, const float* sgate,
                                  const float* res, float* act, float* y, dr_bf16* yb, int rows, int h, int i,
                                  int topk, const float* nw, float eps, dr_stream_t st);
+/* The FP8 small-batch path with the router in the gate_up launch: dr_router_topk_rows followed
+ * by dr_moe_decode_rows_fp8(_bf16s) on the same arguments, with the same results bit for bit
+ * (routing bit-exact per row), in two launches per four rows instead of three.  The router's
+ * blocks come first in the gate_up launch; the gate_up blocks request their rows of x and
+ * then wait for the picks, which the router's last block publishes as tagged 64-bit words;
+ * down follows as in dr_moe_decode_rows_fp8.  counter: 4 words, zero before the first call
+ * and then owned by the library (word 1 holds the tag of the last launch); tags: 384 words
+ * (the picks and the launch's block count), zero before the first call and then owned by the
+ * library; logits rows (e + 1) floats; idx / wts / sgate as dr_router_topk_rows; act rows x
+ * (topk + 1) x i floats; y may alias x and res.  e in [topk, 256], topk = 8,
+ * 1 <= rows <= 64.  Calls that share counter or tags must not overlap.  A gate_up block that
+ * sees no picks within its wait limit raises DR_ERR_ROUTE_WAIT (the outputs are then wrong).
+ * No reference counterpart (the engine decodes one token per step). */
+int dr_moe_decode_rows_routed_fp8(const dr_bf16* router_w, const float* nw, float eps, int e, const uint8_t* gu_w,
+                                  const float* gu_s, const uint8_t* d_w, const float* d_s, const int8_t* sgu_q,
+                                  const dr_half* sgu_s, const int8_t* sd_q, const dr_half* sd_s, const float* x,
+                                  float* logits, int* idx, float* wts, float* sgate, uint32_t* counter,
+                                  uint64_t* tags, const float* res, float* act, float* y, int rows, int h, int i,
+                                  int topk, dr_stream_t st);
+int dr_moe_decode_rows_routed_fp8_bf16s(const dr_bf16* router_w, const float* nw, float eps, int e,
+                                        const uint8_t* gu_w, const dr_bf16* gu_s, const uint8_t* d_w,
+                                        const dr_bf16* d_s, const int8_t* sgu_q, const dr_bf16* sgu_s,
+                                        const int8_t* sd_q, const dr_bf16* sd_s, const float* x, float* logits,
+                                        int* idx, float* wts, float* sgate, uint32_t* counter, uint64_t* tags,
+                                        const float* res, float* act, float* y, dr_bf16* yb, int rows, int h,
+                                        int i, int topk, dr_stream_t st);
 
 /* Single int4 GEMV (benchmark configuration 1): y[n] = sum_k (q[n,k] scale + min) x[k] with
  * x bf16, bf16 (scale, min) pairs per 64-group, fp32 accumulation; y f32 and (nullable) yb

@@ -51,6 +51,19 @@ def test_error_strings_and_shape_errors_without_gpu():
     assert lib.raw("dr_moe_prefill_rows_bf16s")(*([None] * 4), None, 300, None, None, None, None, None, 256, 4096,
                                                 512, None) == -1
     assert lib.raw("dr_gemv_q4_bf16s")(None, None, None, None, None, 10, 1000, None) == -1
+    # fused small-batch FP8 router + experts: (router_w, nw, eps, e, 8 weight pointers, x, logits, idx,
+    # wts, sgate, counter, tags, res, act, y, yb, rows, h, i, topk, st); shapes are rejected before
+    # any pointer is used, then null router / buffers
+    f = lib.raw("dr_moe_decode_rows_routed_fp8_bf16s")
+    base = [1, 1, 1e-6, 256] + [1] * 19 + [4, 2048, 512, 8, None]
+    for pos, bad in ((3, 7), (3, 257), (23, 0), (23, 65), (24, 1024), (25, 256), (26, 4)):
+        a = list(base)
+        a[pos] = bad
+        assert f(*a) == -1, (pos, bad)
+    for pos in (0, 13, 17, 18):
+        a = list(base)
+        a[pos] = None
+        assert f(*a) == -1, pos
 
 
 def _rust_decls(text):

@@ -159,3 +159,66 @@ def test_cfg5_fp8_batch4_rows_path_full_size(fmt):
         assert_close(gy[r], ry, what=f"batch-4 row {r}")
     del Ld
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fmt,rows", [("cfg", 4), ("ref", 4), ("cfg", 5), ("cfg", 1), ("cfg", 3)])
+def test_routed_fp8_rows_equal_three_launch_path(fmt, rows):
+    """dr_moe_decode_rows_routed_fp8(_bf16s) (router + top-k in the gate_up launch, then down)
+    against
+    dr_router_topk_rows + dr_moe_decode_rows_fp8(_bf16s) on the same inputs: logits, picks,
+    weights, shared gates, activations and outputs bit for bit (both run the same arithmetic),
+    over three calls in a row with different x on one counter and tag buffer (each launch tags
+    its picks afresh), the last with y aliasing x and res."""
+    import torch
+
+    from test_gpu_configs import fp8_layer_gpu
+
+    E = 256
+    Ld = fp8_layer_gpu(71 if fmt == "cfg" else 72, fmt)
+    L, P, sp = D.lib(), D.ptr, D.stream_ptr()
+    wargs = [P(Ld[k]) for k in ("gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")]
+    z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
+    counter, tags = z(4, torch.int32), z(384, torch.int64)
+    c3 = z(4, torch.int32)
+    rng = np.random.default_rng(70 + rows)
+    for call in range(3):
+        x = rng.normal(0, 1, (rows, H)).astype(np.float32)
+        outs = []
+        for fused in (False, True):
+            dx = dev(x)
+            lg, idx, wts, sg = z(rows * (E + 1)), z(rows * TOPK, torch.int32), z(rows * TOPK), z(rows)
+            act = z(rows * (TOPK + 1) * I)
+            y = dx if call == 2 else z(rows * H)
+            yb = z(rows * H, torch.int16)
+            if fused:
+                if fmt == "cfg":
+                    rc = L.dr_moe_decode_rows_routed_fp8_bf16s(P(Ld["router"]), P(Ld["nw"]), 1e-6, E, *wargs, P(dx),
+                                                               P(lg), P(idx), P(wts), P(sg), P(counter), P(tags), P(dx),
+                                                               P(act), P(y), P(yb), rows, H, I, TOPK, sp)
+                else:
+                    rc = L.dr_moe_decode_rows_routed_fp8(P(Ld["router"]), P(Ld["nw"]), 1e-6, E, *wargs, P(dx), P(lg),
+                                                         P(idx), P(wts), P(sg), P(counter), P(tags), P(dx), P(act),
+                                                         P(y), rows, H, I, TOPK, sp)
+                assert rc == 0
+            else:
+                assert L.dr_router_topk_rows(P(Ld["router"]), P(dx), P(Ld["nw"]), 1e-6, P(lg), E, TOPK, H, rows,
+                                             P(idx), P(wts), P(sg), P(c3), sp) == 0
+                args = [*wargs, P(dx), P(idx), P(wts), P(sg), P(dx), P(act), P(y)]
+                if fmt == "cfg":
+                    rc = L.dr_moe_decode_rows_fp8_bf16s(*args, P(yb), rows, H, I, TOPK, P(Ld["nw"]), 1e-6, sp)
+                else:
+                    rc = L.dr_moe_decode_rows_fp8(*args, rows, H, I, TOPK, P(Ld["nw"]), 1e-6, sp)
+                assert rc == 0
+            torch.cuda.synchronize()
+            assert L.dr_last_error() == 0
+            outs.append([host(t) for t in (lg, idx, wts, sg, act, y, yb)])
+        for name, a, b in zip(("logits", "idx", "wts", "sgate", "act", "y", "yb"), *outs):
+            np.testing.assert_array_equal(bits(a) if a.dtype == np.float32 else a,
+                                          bits(b) if b.dtype == np.float32 else b, err_msg=f"call {call}: {name}")
+        assert int(host(counter)[0]) == 0 and int(host(counter)[2]) == 0
+    # one tag per chunk of four rows
+    assert int(host(counter)[1]) == 3 * ((rows + 3) // 4)
+    assert not host(tags)[128:].any()  # the launch's block counters are back at zero
+    del Ld
+    torch.cuda.empty_cache()
+

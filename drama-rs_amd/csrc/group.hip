@@ -1,12 +1,14 @@
 // Prefill grouping of (row, k) pairs by expert (reference: kernels/drama.cu:744-797,
 // src/engine.rs:564-575) and the weighted combine.
 //
-// dr_moe_group is one workgroup of 16 waves: a stable counting sort in three phases.
+// dr_moe_group is one workgroup of 16 waves: a stable counting sort in three phases, each wave's
+// expert ids loaded once, all at the start (one memory round trip).
 //   1. wave w takes chunks of 128 pairs; for each 64-pair half it finds, with 8 ballots over
 //      the expert-id bits, the lanes that share its expert: the rank within the chunk is the
 //      count of lower such lanes, the chunk count goes to a [chunk][expert] table in LDS;
-//   2. thread e scans its expert's column over the chunks (exclusive), giving each chunk's
-//      base and the expert's total; a block scan over experts gives the offsets;
+//   2. four threads per expert scan its column over the chunks (exclusive, 16 chunks each,
+//      then across the four), giving each chunk's base and the expert's total; a block scan
+//      over experts gives the offsets;
 //   3. slot = offsets[e] + base[chunk][e] + rank.
 // The order within an expert is ascending pair index (the reference's atomics give an
 // unspecified order; this is one of its possible outcomes, and the CPU oracle's).
@@ -41,17 +43,28 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
                      int topk) {
   __shared__ uint16_t tab[GR_MAXCH][256];  // per-chunk count, then per-chunk base
   __shared__ uint8_t rank[GR_MAXN];
-  __shared__ int s_off[256];
+  __shared__ int s_off[256], s_tot[256];
   __shared__ int s_wsum[GR_WAVES];
   const int lane = lane_id(), wave = wave_id();
   const int nch = (n + GR_CHUNK - 1) / GR_CHUNK;
-  for (int i = threadIdx.x; i < GR_MAXCH * 256; i += GR_THREADS) (&tab[0][0])[i] = 0;
+  // every expert id this wave handles (chunks wave + 16 cc, both halves), requested at once:
+  // one memory round trip instead of one per chunk half and pass
+  constexpr int NKEY = GR_MAXCH / GR_WAVES * 2;
+  uint32_t keys[NKEY];
+#pragma unroll
+  for (int j = 0; j < NKEY; ++j) {
+    const int i = (wave + GR_WAVES * (j >> 1)) * GR_CHUNK + (j & 1) * 64 + lane;
+    keys[j] = i < n ? (uint32_t)ld(i) & 255u : 0u;  // ids must be < E <= 256
+  }
+  for (int i = threadIdx.x; i < nch * 64; i += GR_THREADS) reinterpret_cast<uint64_t*>(&tab[0][0])[i] = 0;
   __syncthreads();
-  for (int c = wave; c < nch; c += GR_WAVES) {
-    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+  for (int j = 0; j < NKEY; ++j) {
+    const int c = wave + GR_WAVES * (j >> 1), h = j & 1;
+    if (c < nch) {
       const int i = c * GR_CHUNK + h * 64 + lane;
       const bool valid = i < n;
-      const uint32_t key = valid ? (uint32_t)ld(i) & 255u : 0u;  // ids must be < E <= 256
+      const uint32_t key = keys[j];
       const uint64_t m = match8(key, valid);
       const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
       const int r = __popcll(m & lower);
@@ -66,16 +79,34 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
     }
   }
   __syncthreads();
-  // phase 2: per-expert exclusive scan over chunks; totals
-  int total = 0;
-  if (threadIdx.x < 256) {
-    const int e = threadIdx.x;
-    for (int c = 0; c < nch; ++c) {
-      const int v = tab[c][e];
-      tab[c][e] = (uint16_t)total;
-      total += v;
+  // phase 2: per-expert exclusive scan over chunks, four threads per expert (chunks
+  // 16 q .. 16 q + 15 each, read at once), combined across the four lanes; totals
+  {
+    static_assert(GR_THREADS == 4 * 256 && GR_MAXCH == 4 * 16, "four scan threads per expert");
+    const int e = threadIdx.x >> 2, q = threadIdx.x & 3;
+    int v[16], loc = 0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v[t] = 16 * q + t < nch ? (int)tab[16 * q + t][e] : 0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int c = v[t];
+      v[t] = loc;
+      loc += c;
     }
+    int inc = loc;
+    int u = __shfl_up(inc, 1, 4);
+    if (q >= 1) inc += u;
+    u = __shfl_up(inc, 2, 4);
+    if (q >= 2) inc += u;
+    const int base = inc - loc;
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      if (16 * q + t < nch) tab[16 * q + t][e] = (uint16_t)(v[t] + base);
+    if (q == 3) s_tot[e] = inc;
   }
+  __syncthreads();
+  int total = 0;
+  if (threadIdx.x < 256) total = s_tot[threadIdx.x];
   // block-wide exclusive scan of totals over experts 0..255 (waves 0..3)
   if (threadIdx.x < 256) {
     int v = total;
@@ -104,11 +135,15 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += GR_THREADS) {
-    const int e = ld(i) & 255, c = i / GR_CHUNK;
-    const int slot = s_off[e] + (int)tab[c][e] + (int)rank[i];
-    slot_of[i] = slot;
-    if (row_of_slot) row_of_slot[slot] = i / topk;
+#pragma unroll
+  for (int j = 0; j < NKEY; ++j) {
+    const int c = wave + GR_WAVES * (j >> 1), i = c * GR_CHUNK + (j & 1) * 64 + lane;
+    if (i < n) {
+      const int e = (int)keys[j];
+      const int slot = s_off[e] + (int)tab[c][e] + (int)rank[i];
+      slot_of[i] = slot;
+      if (row_of_slot) row_of_slot[slot] = i / topk;
+    }
   }
 }
 

@@ -457,6 +457,17 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
     const uint4* xrow = xb + (size_t)c16 * (K / 8);
     // int4 pairs: first 8-input token block of this lane's swapped words (see compute)
     const int tb = 4 * (g & 1) + 2 * (g >> 1);
+    // token block (16 P + j) ^ c16 = 16 P + (j ^ c16) for j < 16: per-lane bases for the j this
+    // lane reads, so 16 P becomes the LDS instruction's immediate offset (no address arithmetic
+    // per read)
+    const uint4* xj0 = xrow + ((tb) ^ c16);
+    const uint4* xj1 = xrow + ((tb + 1) ^ c16);
+    const uint4* xj8 = xrow + ((tb + 8) ^ c16);
+    const uint4* xj9 = xrow + ((tb + 9) ^ c16);
+    const uint4* xu0 = xrow + ((2 * g) ^ c16);
+    const uint4* xu1 = xrow + ((2 * g + 1) ^ c16);
+    const uint4* xu8 = xrow + ((8 + 2 * g) ^ c16);
+    const uint4* xu9 = xrow + ((9 + 2 * g) ^ c16);
     f32x4 tA = {0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const Step<F>& sa, int G0) {
       if constexpr (F::paired) {
@@ -487,10 +498,10 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
           const auto s02 = __builtin_amdgcn_permlane32_swap(sa.raw[pp].x, sa.raw[pp].z, false, false);
           const auto s13 = __builtin_amdgcn_permlane32_swap(sa.raw[pp].y, sa.raw[pp].w, false, false);
           const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 ua = mfma(xrow[(16 * P + tb + 1) ^ c16], q4_frag(s13[0], q_mask, q_bias),
-                                mfma(xrow[(16 * P + tb) ^ c16], q4_frag(s02[0], q_mask, q_bias), z4));
-          const f32x4 ub = mfma(xrow[(16 * P + tb + 9) ^ c16], q4_frag(s13[1], q_mask, q_bias),
-                                mfma(xrow[(16 * P + tb + 8) ^ c16], q4_frag(s02[1], q_mask, q_bias), z4));
+          const f32x4 ua = mfma(xj1[16 * P], q4_frag(s13[0], q_mask, q_bias),
+                                mfma(xj0[16 * P], q4_frag(s02[0], q_mask, q_bias), z4));
+          const f32x4 ub = mfma(xj9[16 * P], q4_frag(s13[1], q_mask, q_bias),
+                                mfma(xj8[16 * P], q4_frag(s02[1], q_mask, q_bias), z4));
           const uint32_t sw[4] = {sa.sc.x, sa.sc.y, sa.sc.z, sa.sc.w};
           const float sca = F::scale_val(sw[2 * pp]).x, scb = F::scale_val(sw[2 * pp + 1]).x;
 #pragma unroll
@@ -503,7 +514,8 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int G = G0 + i;
-          const uint4 x0 = xrow[(G * 8 + 2 * g) ^ c16], x1 = xrow[(G * 8 + 2 * g + 1) ^ c16];
+          // (G * 8 + 2 g + j) ^ c16 = 16 (G >> 1) + ((8 (G & 1) + 2 g + j) ^ c16)
+          const uint4 x0 = (G & 1 ? xu8 : xu0)[16 * (G >> 1)], x1 = (G & 1 ? xu9 : xu1)[16 * (G >> 1)];
           const f32x4 z = {0.f, 0.f, 0.f, 0.f};
           uint4 a0, a1;
           F::convert(sa.raw[i], a0, a1);

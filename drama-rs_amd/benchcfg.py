@@ -367,7 +367,7 @@ def config5_fp8(lib, st, iters=100, copies=4):
                                     "dr_moe_decode_rows_fp8_bf16s, 3 launches); bytes = router + distinct "
                                     "experts + shared + vectors; us_graph: replayed from a HIP graph")
     # the same with the router in the gate_up launch (2 launches)
-    c4, tags4 = z(4, torch.int32), z(384, torch.int64)
+    c4, tags4 = z(4, torch.int32), z(896, torch.int64)
 
     def b4f(i):
         Lc = Ls[i % copies]

@@ -37,45 +37,37 @@ DEV void unpack16(const float4* xs, int lane, float (&xa)[16], float (&xb)[16], 
   }
 }
 
-// gate_up of B decode rows.  Routed units are (row b, pick k, pair j), j fastest; the NBR
-// routed blocks' waves walk them spaced by the grid (wave g takes units g, g + NW, ..., so
-// waves running side by side read neighbouring rows of one expert), keeping D units in flight
-// and loading unit p + D once unit p is computed.  The shared-expert blocks that follow (PPWS
-// pairs per wave, all loaded at once) serve all B rows with one read of their weights.  x
-// (and the norm weight) are requested before the weights, so the staging overlaps the fetch.
-// Block blk of the gate_up grid (shared blocks first); the picks come from Picks: wait() is
-// called by every thread of a routed block once its x is requested, get(i) returns pick i.
-template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B, class Picks>
-DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* __restrict__ S,
-                           const int8_t* __restrict__ shq, const uint16_t* __restrict__ shs, const float* x,
-                           const Picks& picks, float* __restrict__ act, const float* nw, float eps, float4* xs) {
-  constexpr int H = H8, I = I8, NT = WPB * 64, NW = NBR * WPB, PPW = B * TOPK8 * I / NW;
+// gate_up of B decode rows.  Routed units are (row b, pick k, pair j), j fastest; the routed
+// waves walk them spaced by the grid (wave g of NW takes units g, g + NW, ..., so waves running
+// side by side read neighbouring rows of one expert), keeping D units in flight and loading
+// unit p + D once unit p is computed.  The shared expert's pairs (PPWS per wave, all loaded at
+// once) serve all B rows with one read of their weights.  Both read x̂ staged in LDS by XStage.
+template <int SF, int D, int B, int NW>
+struct RoutedFP8 {
+  static constexpr int H = H8, I = I8, PPW = B * TOPK8 * I / NW;
   static_assert(PPW * NW == B * TOPK8 * I && D <= PPW, "units split evenly over the routed waves");
-  constexpr int NBS = I / (WPB * PPWS);  // shared-expert blocks, dispatched first
-  const int lane = lane_id(), wave = wave_id();
-  if (blk >= NBS) {
-    const int g = (blk - NBS) * WPB + wave;
-    XStage<H, NT, B, SlotQ8H> xst;
-    xst.load(x, nw);
-    picks.wait();
-    uint4 g0[D], g1[D], u0[D], u1[D];
-    uint32_t sr[D][4];
-    auto issue = [&](int p, int d) {
-      const int u = g + NW * p, b = u / (TOPK8 * I), k = (u / I) % TOPK8, j = u % I;
-      const size_t e = (size_t)picks.get(b * TOPK8 + k);
-      const uint8_t* rg = W + (e * (2 * I) + j) * H + lane * 16;
-      const uint8_t* ru = rg + (size_t)I * H;
-      g0[d] = ld16(rg), g1[d] = ld16(rg + 1024), u0[d] = ld16(ru), u1[d] = ld16(ru + 1024);
-      const size_t sb = e * (size_t)(2 * I / 128) * (H / 128);
-      sr[d][0] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + (lane >> 3));
-      sr[d][1] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + 8 + (lane >> 3));
-      sr[d][2] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + (lane >> 3));
-      sr[d][3] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + 8 + (lane >> 3));
-      __builtin_amdgcn_sched_barrier(0);
-    };
-#pragma unroll
-    for (int p = 0; p < D; ++p) issue(p, p);
-    xst.finish(nw != nullptr, eps, xs);
+  uint4 g0[D], g1[D], u0[D], u1[D];
+  uint32_t sr[D][4];
+  template <class Picks>
+  DEV void issue(const uint8_t* __restrict__ W, const void* __restrict__ S, const Picks& picks, int g, int p, int d) {
+    const int lane = lane_id();
+    const int u = g + NW * p, b = u / (TOPK8 * I), k = (u / I) % TOPK8, j = u % I;
+    const size_t e = (size_t)picks.get(b * TOPK8 + k);
+    const uint8_t* rg = W + (e * (2 * I) + j) * H + lane * 16;
+    const uint8_t* ru = rg + (size_t)I * H;
+    g0[d] = ld16(rg), g1[d] = ld16(rg + 1024), u0[d] = ld16(ru), u1[d] = ld16(ru + 1024);
+    const size_t sb = e * (size_t)(2 * I / 128) * (H / 128);
+    sr[d][0] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + (lane >> 3));
+    sr[d][1] = blk_raw<SF>(S, sb + (size_t)(j >> 7) * (H / 128) + 8 + (lane >> 3));
+    sr[d][2] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + (lane >> 3));
+    sr[d][3] = blk_raw<SF>(S, sb + (size_t)((I + j) >> 7) * (H / 128) + 8 + (lane >> 3));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // units 0 .. D - 1 issued, x̂ staged
+  template <class Picks>
+  DEV void run(const uint8_t* __restrict__ W, const void* __restrict__ S, const Picks& picks, int g,
+               const float4* xs, float* __restrict__ act) {
+    const int lane = lane_id();
 #pragma unroll
     for (int p = 0; p < PPW; ++p) {
       const int d = p % D;
@@ -85,17 +77,21 @@ DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* _
       opaque(g0[d]), opaque(g1[d]), opaque(u0[d]), opaque(u1[d]);
       float gv = blk_cvt<SF>(sr[d][0]) * dot16_fp8(g0[d], xa, 0.f) + blk_cvt<SF>(sr[d][1]) * dot16_fp8(g1[d], xb, 0.f);
       float uv = blk_cvt<SF>(sr[d][2]) * dot16_fp8(u0[d], xa, 0.f) + blk_cvt<SF>(sr[d][3]) * dot16_fp8(u1[d], xb, 0.f);
-      if (p + D < PPW) issue(p + D, d);
+      if (p + D < PPW) issue(W, S, picks, g, p + D, d);
       gv = wave_sum(gv);
       uv = wave_sum(uv);
       if (lane == 0) act[(size_t)b * (TOPK8 + 1) * I + k * I + j] = silu(gv) * uv;
     }
-  } else {
-    const int j0 = (blk * WPB + wave) * PPWS;
-    XStage<H, NT, B, SlotQ8H> xst;
-    xst.load(x, nw);
-    uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
-    float sg0[PPWS], sg1[PPWS], su0[PPWS], su1[PPWS];
+  }
+};
+
+template <class SH, int PPWS, int B>
+struct SharedFP8 {
+  static constexpr int H = H8, I = I8;
+  uint4 g0[PPWS], g1[PPWS], u0[PPWS], u1[PPWS];
+  float sg0[PPWS], sg1[PPWS], su0[PPWS], su1[PPWS];
+  DEV void load(const int8_t* __restrict__ shq, const uint16_t* __restrict__ shs, int j0) {
+    const int lane = lane_id();
 #pragma unroll
     for (int p = 0; p < PPWS; ++p) {
       const uint8_t* rg = reinterpret_cast<const uint8_t*>(shq) + (size_t)(j0 + p) * H + lane * 16;
@@ -108,7 +104,9 @@ DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* _
       sg0[p] = SH::scale(shs, j, lane * 16, H), sg1[p] = SH::scale(shs, j, 1024 + lane * 16, H);
       su0[p] = SH::scale(shs, I + j, lane * 16, H), su1[p] = SH::scale(shs, I + j, 1024 + lane * 16, H);
     }
-    xst.finish(nw != nullptr, eps, xs);
+  }
+  DEV void run(const float4* xs, float* __restrict__ act, int j0) {
+    const int lane = lane_id();
 #pragma unroll 1
     for (int r = 0; r < B; ++r) {
       pin_weights(g0, g1, u0, u1);  // converted per row, not hoisted out of the row loop
@@ -124,6 +122,35 @@ DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* _
         if (lane == 0) ar[p] = silu(g) * u;
       }
     }
+  }
+};
+
+// Block blk of the gate_up grid: NBS shared-expert blocks first, then the NBR routed blocks.
+// x (and the norm weight) are requested before the weights, so the staging overlaps the
+// fetch; a routed block's picks come from Picks (wait() by every thread, get(i) = pick i).
+template <int SF, class SH, int WPB, int NBR, int D, int PPWS, int B, class Picks>
+DEV void gate_up_fp8_block(int blk, const uint8_t* __restrict__ W, const void* __restrict__ S,
+                           const int8_t* __restrict__ shq, const uint16_t* __restrict__ shs, const float* x,
+                           const Picks& picks, float* __restrict__ act, const float* nw, float eps, float4* xs) {
+  constexpr int NT = WPB * 64, NW = NBR * WPB;
+  constexpr int NBS = I8 / (WPB * PPWS);  // shared-expert blocks, dispatched first
+  const int wave = wave_id();
+  XStage<H8, NT, B, SlotQ8H> xst;
+  xst.load(x, nw);
+  if (blk >= NBS) {
+    const int g = (blk - NBS) * WPB + wave;
+    picks.wait();
+    RoutedFP8<SF, D, B, NW> ru;
+#pragma unroll
+    for (int p = 0; p < D; ++p) ru.issue(W, S, picks, g, p, p);
+    xst.finish(nw != nullptr, eps, xs);
+    ru.run(W, S, picks, g, xs, act);
+  } else {
+    const int j0 = (blk * WPB + wave) * PPWS;
+    SharedFP8<SH, PPWS, B> sh;
+    sh.load(shq, shs, j0);
+    xst.finish(nw != nullptr, eps, xs);
+    sh.run(xs, act, j0);
   }
 }
 
@@ -142,8 +169,9 @@ __global__ void __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(W
   gate_up_fp8_block<SF, SH, WPB, NBR, D, PPWS, B>(blockIdx.x, W, S, shq, shs, x, PicksGlobal{idx}, act, nw, eps, xs);
 }
 
-// The picks of the fused router + gate_up launch: wave 0 of the block polls the B * 8 tagged
-// words (tag << 32) | expert that the router's last block publishes, until every tag is the
+// The picks of the fused router + gate_up launch: wave 0 of the block polls its replica of the
+// B * 8 tagged words (tag << 32) | expert that the router's last block publishes, until every
+// tag is the
 // launch's (bounded: on time-out DR_ERR_ROUTE_WAIT is raised and expert 0 is used), and leaves
 // the experts in LDS for the block.
 template <int B>
@@ -156,9 +184,11 @@ struct PicksTagged {
     constexpr int n = B * TOPK8;
     if (wave_id() == 0) {
       const int lane = lane_id();
+      // this block's replica of the experts (router_rows.hpp)
+      const uint64_t* rep = tags + RR_WORD0 + 32 * (blockIdx.x % RR_REPS);
       uint64_t v = (uint64_t)tag << 32;
       for (int it = 0;; ++it) {
-        if (lane < n) v = __hip_atomic_load(tags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < n) v = __hip_atomic_load(rep + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__ballot((uint32_t)(v >> 32) != tag) == 0) break;
         if (it == (1 << 20)) {
           if (lane == 0) raise_err(err, kErrRouteWait);
@@ -179,9 +209,9 @@ struct PicksTagged {
 // 128-byte line in the tags buffer after the picks, and the block that fills its group adds
 // one to a top counter; the block that fills the top is the launch's last.  Counters start at
 // zero and the last block resets them.
-constexpr int RC_G = 16, RC_DONE = 128, RC_WORDS = RC_DONE + 16 * RC_G;
-static_assert(RC_WORDS == 384, "the tags buffer size the header states");
-static_assert(RC_DONE >= 4 * (2 * TOPK8 + 1), "picks before the counters");
+constexpr int RC_G = 16, RC_DONE = RR_WORD0 + 32 * RR_REPS, RC_WORDS = RC_DONE + 16 * RC_G;
+static_assert(RC_WORDS == 896, "the tags buffer size the header states");
+static_assert(RR_WORD0 >= 4 * (2 * TOPK8 + 1) && 4 * TOPK8 <= 32, "picks, then their replicas, then the counters");
 DEV uint32_t* rc_ctr(uint64_t* tags, int base, int g) { return reinterpret_cast<uint32_t*>(tags + base + 16 * g); }
 DEV uint32_t rc_n(int nb, int g) { return (uint32_t)(nb / RC_G + (g < nb % RC_G ? 1 : 0)); }
 // one thread per block; true for the block that completes the count
@@ -210,15 +240,17 @@ DEV void launch_done(uint64_t* tags, uint32_t* counter, int blk, int nb, uint32_
   }
 }
 
-// Router, top-k and gate_up of B decode rows in one launch.  Blocks [0, NRB) run the router
-// of router_rows.hpp (its last block publishes the picks as tagged words), then the gate_up
-// grid of k_moe_gate_up_fp8 follows: its shared-expert blocks need no picks, its routed blocks
-// request their x and then wait for the picks.  A block waits only for blocks of lower index,
-// which are dispatched first, so the launch needs no co-residency.  counter: [0] the router's
-// arrivals (reset by its last block), [1] the tag of the previous launch, [2] the top of the
-// finished-block count (launch_done), whose last block advances [1], so every launch tags its
-// picks afresh.
-template <int SF, class SH, int NBR, int D, int PPWS, int B>
+// Router, top-k and gate_up of B decode rows in one launch of RG_BLOCKS blocks, one per
+// routed gate_up slice: every wave takes B units (RoutedFP8, D in flight) once the picks are
+// there.  Before that, blocks [0, NRB) run the router of router_rows.hpp (its last block
+// publishes the picks as tagged words) and blocks [NRB, NRB + RG_NBS) the shared expert's
+// pairs (which need no picks), so the router's and the shared expert's time is spent while the
+// picks are awaited, and no block waits for a free slot (two blocks per CU hold the grid).
+// Wave 0 of each block polls the picks.  counter: [0] the router's arrivals (reset by its last
+// block), [1] the tag of the previous launch, [2] the top of the finished-block count
+// (launch_done), whose last block advances [1], so every launch tags its picks afresh.
+constexpr int RG_BLOCKS = 512, RG_PPWS = 2, RG_NBS = I8 / (8 * RG_PPWS);
+template <int SF, class SH, int D, int B>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
     k_moe_route_gate_up_fp8(const uint16_t* __restrict__ RW, float* __restrict__ logits, int E,
                             int* __restrict__ idx, float* __restrict__ wts, float* __restrict__ sgate,
@@ -232,15 +264,33 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
   if (threadIdx.x == 0) s_tag = __hip_atomic_load(counter + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   __syncthreads();
   const uint32_t tag = s_tag;
+  const int blk = blockIdx.x, wave = wave_id();
   const int nrb = (E + RT_WPB) / RT_WPB;
-  if ((int)blockIdx.x < nrb) {
-    router_rows_block<B>(blockIdx.x, nrb, RW, x, nw, eps, logits, E, TOPK8, idx, wts, sgate, counter, tags, tag,
+  if (blk < nrb) {
+    router_rows_block<B>(blk, nrb, RW, x, nw, eps, logits, E, TOPK8, idx, wts, sgate, counter, tags, tag,
                          reinterpret_cast<float4(*)[H8 / 4]>(xs));
-  } else {
-    gate_up_fp8_block<SF, SH, 8, NBR, D, PPWS, B>(blockIdx.x - nrb, W, S, shq, shs, x,
-                                                  PicksTagged<B>{tags, tag, s_idx, err}, act, nw, eps, xs);
+    __syncthreads();  // the router's staging in xs is done with
   }
-  if (wave_id() == 0) launch_done(tags, counter, blockIdx.x, gridDim.x, tag);
+  XStage<H8, 512, B, SlotQ8H> xst;
+  xst.load(x, nw);
+  const bool shared = blk >= nrb && blk < nrb + RG_NBS;
+  const int j0 = ((blk - nrb) * 8 + wave) * RG_PPWS;
+  if (shared) {
+    SharedFP8<SH, RG_PPWS, B> sh;
+    sh.load(shq, shs, j0);
+    xst.finish(nw != nullptr, eps, xs);
+    sh.run(xs, act, j0);
+  } else {
+    xst.finish(nw != nullptr, eps, xs);
+  }
+  const PicksTagged<B> picks{tags, tag, s_idx, err};
+  picks.wait();
+  const int g = blk * 8 + wave;
+  RoutedFP8<SF, D, B, RG_BLOCKS * 8> ru;
+#pragma unroll
+  for (int p = 0; p < D; ++p) ru.issue(W, S, picks, g, p, p);
+  ru.run(W, S, picks, g, xs, act);
+  if (wave == 0) launch_done(tags, counter, blk, RG_BLOCKS, tag);
 }
 
 // The down weights of output rows n0 .. n0 + RPW - 1: per row the 8 routed expert rows of
@@ -414,15 +464,13 @@ int launch_decode_routed_fp8(const uint16_t* rw, float* logits, int E, int* idx,
   if (H != H8 || I != I8 || topk != TOPK8 || rows < 1 || rows > 64 || E < TOPK8 || E > 256) return -1;
   if (!rw || !logits || !idx || !wts || !sgate || !counter || !tags) return -1;
   uint32_t* err = err_word();
-  constexpr int NBR = 512, PPWS = 2, NBS = I8 / (8 * PPWS);
-  const int nrb = (E + RT_WPB) / RT_WPB;
   for (int r0 = 0; r0 < rows; r0 += 4) {
     const int b = rows - r0 < 4 ? rows - r0 : 4;
     const size_t xo = (size_t)r0 * H, ko = (size_t)r0 * topk, ao = (size_t)r0 * (topk + 1) * I;
     float* lg = logits + (size_t)r0 * (E + 1);
     auto go = [&](auto kb) {
       constexpr int KB = decltype(kb)::value, D = KB < 2 ? KB : 2, DW = KB == 1 ? 4 : 8, DR = 2;
-      hipLaunchKernelGGL((k_moe_route_gate_up_fp8<SF, SH, NBR, D, PPWS, KB>), dim3(nrb + NBS + NBR), dim3(512), 0, st,
+      hipLaunchKernelGGL((k_moe_route_gate_up_fp8<SF, SH, D, KB>), dim3(RG_BLOCKS), dim3(512), 0, st,
                          rw, lg, E, idx + ko, wts + ko, sgate + r0, counter, tags, err, gu_w, gu_s, sgu_q, sgu_s,
                          x + xo, act + ao, nw, eps);
       hipLaunchKernelGGL((k_moe_down_fp8<SF, SH, DW, DR>), dim3(H8 / (DW * DR), KB), dim3(DW * 64), 0, st, d_w, d_s,

@@ -9,12 +9,13 @@
 // of canon.hpp, so each row's logits, picks and weights equal those of dr_router_topk on that
 // row.  Logits are published with cache-bypassing (sc1) stores; each block counts itself in
 // once its stores completed, and the last block loads the logits of all rows at once and
-// spreads the per-row work over its waves: for topk <= 8 the 4 B group selections and B
-// softmax denominators, then one rank merge per row; for topk > 8 one wave per row.  It
+// spreads the per-row work over its waves: for topk <= 8 the 4 B group selections, then one
+// rank merge per row (whose picks go out at once) beside the B softmax denominators, then
+// the weights; for topk > 8 one wave per row.  It
 // writes idx, wts and sgate, and (tags != nullptr) also publishes them as tagged words
 // (tag << 32) | value bits with cache-bypassing stores, for blocks of the same launch to poll:
-// row r's experts at tags[r topk ..], its weights at tags[(B + r) topk ..], its shared-expert
-// gate logit at tags[2 B topk + r].
+// row r's experts at tags[r topk ..] (and, for B topk <= 32, in RR_REPS replicas), its
+// weights at tags[(B + r) topk ..], its shared-expert gate logit at tags[2 B topk + r].
 // It resets the counter.  Every thread returns normally (no early exit), so callers may add
 // work after it.
 #pragma once
@@ -23,6 +24,9 @@
 namespace drm {
 
 constexpr int RT_WPB = 8;  // router waves (= logit rows) per block
+// Replicas of the tagged experts for pollers (replica r of word i at tags[RR_WORD0 + 32 r + i],
+// one replica per 256 bytes, B topk <= 32): hundreds of pollers on one cache line serialise.
+constexpr int RR_REPS = 16, RR_WORD0 = 128;
 
 template <int B>
 DEV void router_rows_block(int blk, int nblk, const uint16_t* __restrict__ W, const float* __restrict__ x,
@@ -124,22 +128,47 @@ DEV void router_rows_block(int blk, int nblk, const uint16_t* __restrict__ W, co
     }
   };
   if (topk <= 8) {
-    for (int t = wave; t < 5 * B; t += RT_WPB) {
-      const int r = t / 5, sub = t - 5 * r;
-      if (sub < 4) {
-        int ck, ce;
-        canon_select_group8(lg[r], E, sub, &ck, &ce);
-        if (lane < 8) s_cand[r][sub * 8 + lane] = canon_cand64(ck, ce);
+    // the 4 B group selections first, then each row's rank merge (its picks are published at
+    // once: the gate_up blocks of the fused launch wait for them) beside the B softmax
+    // denominators, then the weights
+    for (int t = wave; t < 4 * B; t += RT_WPB) {
+      int ck, ce;
+      canon_select_group8(lg[t >> 2], E, t & 3, &ck, &ce);
+      if (lane < 8) s_cand[t >> 2][(t & 3) * 8 + lane] = canon_cand64(ck, ce);
+    }
+    __syncthreads();
+    for (int t = wave; t < 2 * B; t += RT_WPB) {
+      if (t < B) {
+        const int id = merge_picks(s_cand[t], s_sel[t], topk);
+        if (lane < topk) {
+          idx[t * topk + lane] = id;
+          if (tags) {
+            const uint64_t v = ((uint64_t)tag << 32) | (uint32_t)id;
+            __hip_atomic_store(tags + t * topk + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (B * topk <= 32) {
+#pragma unroll
+              for (int rp = 0; rp < RR_REPS; ++rp)
+                __hip_atomic_store(tags + RR_WORD0 + 32 * rp + t * topk + lane, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+        }
       } else {
         float m;
-        const float z = canon_softmax_z(lg[r], E, &m);
-        if (lane == 0) s_mz[r][0] = m, s_mz[r][1] = z;
+        const float z = canon_softmax_z(lg[t - B], E, &m);
+        if (lane == 0) s_mz[t - B][0] = m, s_mz[t - B][1] = z;
       }
     }
     __syncthreads();
     for (int r = wave; r < B; r += RT_WPB) {
-      const int id = merge_picks(s_cand[r], s_sel[r], topk);
-      publish(r, id, canon_topk_weight(lg[r][lane < topk ? id : 0], s_mz[r][0], s_mz[r][1], topk));
+      const int id = lane < topk ? s_sel[r][lane] : 0;
+      const float wt = canon_topk_weight(lg[r][id], s_mz[r][0], s_mz[r][1], topk);
+      if (lane < topk) {
+        wts[r * topk + lane] = wt;
+        if (tags)
+          __hip_atomic_store(tags + (B + r) * topk + lane, ((uint64_t)tag << 32) | __float_as_uint(wt),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   } else {
     for (int r = wave; r < B; r += RT_WPB) {

@@ -283,7 +283,7 @@ int dr_moe_decode_rows_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, const
  * blocks come first in the gate_up launch; the gate_up blocks request their rows of x and
  * then wait for the picks, which the router's last block publishes as tagged 64-bit words;
  * down follows as in dr_moe_decode_rows_fp8.  counter: 4 words, zero before the first call
- * and then owned by the library (word 1 holds the tag of the last launch); tags: 384 words
+ * and then owned by the library (word 1 holds the tag of the last launch); tags: 896 words
  * (the picks and the launch's block count), zero before the first call and then owned by the
  * library; logits rows (e + 1) floats; idx / wts / sgate as dr_router_topk_rows; act rows x
  * (topk + 1) x i floats; y may alias x and res.  e in [topk, 256], topk = 8,

@@ -178,7 +178,7 @@ def test_routed_fp8_rows_equal_three_launch_path(fmt, rows):
     L, P, sp = D.lib(), D.ptr, D.stream_ptr()
     wargs = [P(Ld[k]) for k in ("gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")]
     z = lambda n, dt=torch.float32: torch.zeros(n, dtype=dt, device="cuda")
-    counter, tags = z(4, torch.int32), z(384, torch.int64)
+    counter, tags = z(4, torch.int32), z(896, torch.int64)
     c3 = z(4, torch.int32)
     rng = np.random.default_rng(70 + rows)
     for call in range(3):
@@ -218,7 +218,7 @@ def test_routed_fp8_rows_equal_three_launch_path(fmt, rows):
         assert int(host(counter)[0]) == 0 and int(host(counter)[2]) == 0
     # one tag per chunk of four rows
     assert int(host(counter)[1]) == 3 * ((rows + 3) // 4)
-    assert not host(tags)[128:].any()  # the launch's block counters are back at zero
+    assert not host(tags)[640:].any()  # the launch's block counters are back at zero
     del Ld
     torch.cuda.empty_cache()
 

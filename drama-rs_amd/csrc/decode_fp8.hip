@@ -250,6 +250,7 @@ DEV void launch_done(uint64_t* tags, uint32_t* counter, int blk, int nb, uint32_
 // block), [1] the tag of the previous launch, [2] the top of the finished-block count
 // (launch_done), whose last block advances [1], so every launch tags its picks afresh.
 constexpr int RG_BLOCKS = 512, RG_PPWS = 2, RG_NBS = I8 / (8 * RG_PPWS);
+constexpr uint64_t RG_X_DELAY = 300;  // measured: 3 µs ahead of the router rows 8.1 -> 7.8 µs, launch -1 µs
 template <int SF, class SH, int D, int B>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
     k_moe_route_gate_up_fp8(const uint16_t* __restrict__ RW, float* __restrict__ logits, int E,
@@ -271,9 +272,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
                          reinterpret_cast<float4(*)[H8 / 4]>(xs));
     __syncthreads();  // the router's staging in xs is done with
   }
+  const bool shared = blk >= nrb && blk < nrb + RG_NBS;
+  if (blk >= nrb + RG_NBS) {
+    // the routed-only blocks request their x RG_X_DELAY ticks (10 ns) late: their units wait
+    // for the picks anyway, and their 32 KB each would otherwise queue ahead of the router's
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < RG_X_DELAY) __builtin_amdgcn_s_sleep(8);
+  }
   XStage<H8, 512, B, SlotQ8H> xst;
   xst.load(x, nw);
-  const bool shared = blk >= nrb && blk < nrb + RG_NBS;
   const int j0 = ((blk - nrb) * 8 + wave) * RG_PPWS;
   if (shared) {
     SharedFP8<SH, RG_PPWS, B> sh;

@@ -131,15 +131,24 @@ DEV void router_rows_block(int blk, int nblk, const uint16_t* __restrict__ W, co
     // the 4 B group selections first, then each row's rank merge (its picks are published at
     // once: the gate_up blocks of the fused launch wait for them) beside the B softmax
     // denominators, then the weights
-    for (int t = wave; t < 4 * B; t += RT_WPB) {
-      int ck, ce;
-      canon_select_group8(lg[t >> 2], E, t & 3, &ck, &ce);
-      if (lane < 8) s_cand[t >> 2][(t & 3) * 8 + lane] = canon_cand64(ck, ce);
+    constexpr bool kRowWave = 2 * B <= RT_WPB;  // one wave selects a whole row (8 rounds over 256)
+    if constexpr (!kRowWave) {
+      for (int t = wave; t < 4 * B; t += RT_WPB) {
+        int ck, ce;
+        canon_select_group8(lg[t >> 2], E, t & 3, &ck, &ce);
+        if (lane < 8) s_cand[t >> 2][(t & 3) * 8 + lane] = canon_cand64(ck, ce);
+      }
+      __syncthreads();
     }
-    __syncthreads();
     for (int t = wave; t < 2 * B; t += RT_WPB) {
       if (t < B) {
-        const int id = merge_picks(s_cand[t], s_sel[t], topk);
+        int id;
+        if constexpr (kRowWave) {
+          id = canon_select_topk(lg[t], E, topk);
+          if (lane < topk) s_sel[t][lane] = id;
+        } else {
+          id = merge_picks(s_cand[t], s_sel[t], topk);
+        }
         if (lane < topk) {
           idx[t * topk + lane] = id;
           if (tags) {

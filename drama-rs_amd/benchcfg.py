@@ -310,6 +310,19 @@ def config5_fp8(lib, st, iters=100, copies=4):
     out["decode_batch1"] = rec(ms * 1000, b1, us_graph=round(msg * 1000, 2),
                                note="router + fp8 gate_up + down + int8 shared; x evolves per call; 4 layer copies "
                                     "rotated; us_graph: the same calls replayed from a HIP graph")
+    # batch 1 with the router in the gate_up launch (2 launches)
+    c1, tags1 = z(4, torch.int32), z(896, torch.int64)
+
+    def dec_r(i):
+        L = Ls[i % copies]
+        lib.dr_moe_decode_rows_routed_fp8_bf16s(P(L["router"]), P(L["nw"]), 1e-6, E, P(L["gu_q"]), P(L["gu_s"]),
+                                                P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]), P(L["sgu_s"]), P(L["sd_q"]),
+                                                P(L["sd_s"]), P(x), P(logits), P(idx), P(wts), P(sg), P(c1), P(tags1),
+                                                P(x), P(act), P(x), None, 1, H, I, TOPK, sp)
+
+    msr = timed(dec_r, iters, st)
+    out["decode_batch1_routed"] = rec(msr * 1000, b1, note="router + top-k in the gate_up launch, then down "
+                                                           "(dr_moe_decode_rows_routed_fp8_bf16s, 1 row)")
     # the fused persistent step over 40 layers: layer l has its own router (so the routing
     # differs from layer to layer) and the experts of copy l % copies (a layer's 8 experts are
     # one of 4 x 256 3-MiB blocks, so few are still in the MALL from an earlier layer)

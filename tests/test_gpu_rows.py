@@ -161,8 +161,9 @@ def test_cfg5_fp8_batch4_rows_path_full_size(fmt):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("fmt,rows", [("cfg", 4), ("ref", 4), ("cfg", 5), ("cfg", 1), ("cfg", 3)])
-def test_routed_fp8_rows_equal_three_launch_path(fmt, rows):
+@pytest.mark.parametrize("fmt,rows,E", [("cfg", 4, 256), ("ref", 4, 256), ("cfg", 5, 256), ("cfg", 1, 256),
+                                         ("cfg", 3, 256), ("cfg", 4, 64), ("cfg", 2, 9)])
+def test_routed_fp8_rows_equal_three_launch_path(fmt, rows, E):
     """dr_moe_decode_rows_routed_fp8(_bf16s) (router + top-k in the gate_up launch, then down)
     against
     dr_router_topk_rows + dr_moe_decode_rows_fp8(_bf16s) on the same inputs: logits, picks,
@@ -173,7 +174,7 @@ def test_routed_fp8_rows_equal_three_launch_path(fmt, rows):
 
     from test_gpu_configs import fp8_layer_gpu
 
-    E = 256
+    # E < 256: the same weights, the router over the first E experts (rows 0 .. E of its matrix)
     Ld = fp8_layer_gpu(71 if fmt == "cfg" else 72, fmt)
     L, P, sp = D.lib(), D.ptr, D.stream_ptr()
     wargs = [P(Ld[k]) for k in ("gu_q", "gu_s", "d_q", "d_s", "sgu_q", "sgu_s", "sd_q", "sd_s")]

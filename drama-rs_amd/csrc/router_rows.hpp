@@ -9,10 +9,12 @@
 // of canon.hpp, so each row's logits, picks and weights equal those of dr_router_topk on that
 // row.  Logits are published with cache-bypassing (sc1) stores; each block counts itself in
 // once its stores completed, and the last block loads the logits of all rows at once and
-// spreads the per-row work over its waves: for topk <= 8 the 4 B group selections, then one
-// rank merge per row (whose picks go out at once) beside the B softmax denominators, then
-// the weights; for topk > 8 one wave per row.  It
-// writes idx, wts and sgate, and (tags != nullptr) also publishes them as tagged words
+// spreads the per-row work over its waves: for topk <= 8 and 2 B <= RT_WPB one wave selects
+// each row's top-k over all its experts (canon_select_topk) beside the B softmax
+// denominators; above 4 rows the 4 B group selections come first and one rank merge per row
+// replaces the row selection; the picks go out at once, then the weights follow; for topk > 8
+// one wave per row does both.  It writes idx, wts and sgate, and (tags != nullptr) also
+// publishes them as tagged words
 // (tag << 32) | value bits with cache-bypassing stores, for blocks of the same launch to poll:
 // row r's experts at tags[r topk ..] (and, for B topk <= 32, in RR_REPS replicas), its
 // weights at tags[(B + r) topk ..], its shared-expert gate logit at tags[2 B topk + r].

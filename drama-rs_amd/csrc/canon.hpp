@@ -130,31 +130,40 @@ DEV int wave_max_i(int v) {
 }
 
 // Top-k selection over E <= 256 logits by one wave: k rounds of (logit desc, index asc)
-// on canon_logit_key.  Lane k < topk receives the expert of pick k.  Expert e = lane + 64 j
-// lives in lane e % 64, slot j = e / 64, so among equal keys the lowest index is the first
-// lane of the first slot whose ballot is non-empty.  Every pick is a distinct expert below E.
+// on canon_logit_key.  Lane k < topk receives the expert of pick k.  Expert e = 4 lane + j
+// lives in lane e / 4, so among equal keys the lowest index is in the lowest lane holding the
+// key, and within a lane in the lowest slot.  Each lane first sorts its four (key, slot) pairs
+// by (key desc, slot asc); a round then takes the wave maximum of the lane heads, the lowest
+// lane whose head equals it wins, and that lane drops its head (KEY_PICKED moves in behind).
+// Every pick is a distinct expert below E.
 DEV int canon_select_topk(const float* __restrict__ l, int E, int topk) {
   const int lane = lane_id();
-  int key[4];
+  int key[4], slot[4] = {0, 1, 2, 3};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int e = lane + WAVE * j;
+    const int e = 4 * lane + j;
     key[j] = e < E ? canon_logit_key(l[e]) : KEY_PAD;
   }
+  auto cex = [&](int a, int b) {
+    const bool sw = key[b] > key[a] || (key[b] == key[a] && slot[b] < slot[a]);
+    const int ka = key[a], kb = key[b], sa = slot[a], sb = slot[b];
+    key[a] = sw ? kb : ka, key[b] = sw ? ka : kb;
+    slot[a] = sw ? sb : sa, slot[b] = sw ? sa : sb;
+  };
+  cex(0, 1), cex(2, 3), cex(0, 2), cex(1, 3), cex(1, 2);
+  int slots = slot[0] | slot[1] << 2 | slot[2] << 4 | slot[3] << 6;  // slot order, 2 bits each
   int id = 0;
   for (int k = 0; k < topk; ++k) {
-    const int kb = wave_max_i(max(max(key[0], key[1]), max(key[2], key[3])));
-    const uint64_t b0 = __ballot(key[0] == kb), b1 = __ballot(key[1] == kb), b2 = __ballot(key[2] == kb),
-                   b3 = __ballot(key[3] == kb);
-    const int js = b0 ? 0 : b1 ? 1 : b2 ? 2 : 3;
-    const uint64_t bj = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
-    const int ls = (int)__builtin_ctzll(bj);
-    if (lane == ls) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (j == js) key[j] = KEY_PICKED;
-    }
-    if (lane == k) id = ls + WAVE * js;
+    const int kb = wave_max_i(key[0]);
+    const int ls = (int)__builtin_ctzll(__ballot(key[0] == kb));
+    const int js = __builtin_amdgcn_readlane(slots, ls) & 3;
+    const bool win = lane == ls;
+    key[0] = win ? key[1] : key[0];
+    key[1] = win ? key[2] : key[1];
+    key[2] = win ? key[3] : key[2];
+    key[3] = win ? KEY_PICKED : key[3];
+    slots = win ? slots >> 2 : slots;
+    id = lane == k ? 4 * ls + js : id;
   }
   return id;
 }

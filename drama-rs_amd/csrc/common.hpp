@@ -85,7 +85,9 @@ DEV void xchg(float v, float& lo, float& hi) {
   if constexpr (O == 1 || O == 2 || O == 4 || O == 8) {
     constexpr int ctrl = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x141 : 0x140;
     lo = v;
-    hi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+    // bound_ctrl set: with full row and bank masks every lane has a valid source, so it changes
+    // no value, and it lets the compiler fold the move into the combining instruction
+    hi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
   } else if constexpr (O == 16) {
     auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);

@@ -231,8 +231,8 @@ DEV void rs_step(float (&v)[64]) {
     } else {
       constexpr int cx = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x12C : 0x128;
       constexpr int cy = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x124 : 0x128;
-      const float px = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), cx, 0xF, 0xF, false));
-      const float py = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y), cy, 0xF, 0xF, false));
+      const float px = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), cx, 0xF, 0xF, true));
+      const float py = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y), cy, 0xF, 0xF, true));
       v[k] = (lane & O) ? y + py : x + px;
     }
   }

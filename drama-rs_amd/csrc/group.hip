@@ -7,8 +7,9 @@
 //      the expert-id bits, the lanes that share its expert: the rank within the chunk is the
 //      count of lower such lanes, the chunk count goes to a [chunk][expert] table in LDS;
 //   2. four threads per expert scan its column over the chunks (exclusive, 16 chunks each,
-//      then across the four), giving each chunk's base and the expert's total; a block scan
-//      over experts gives the offsets;
+//      the four in different waves so each wave reads whole table rows, then combined
+//      through LDS), giving each chunk's base and the expert's total; a block scan over
+//      experts gives the offsets;
 //   3. slot = offsets[e] + base[chunk][e] + rank.
 // The order within an expert is ascending pair index (the reference's atomics give an
 // unspecified order; this is one of its possible outcomes, and the CPU oracle's).
@@ -56,7 +57,10 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
     const int i = (wave + GR_WAVES * (j >> 1)) * GR_CHUNK + (j & 1) * 64 + lane;
     keys[j] = i < n ? (uint32_t)ld(i) & 255u : 0u;  // ids must be < E <= 256
   }
-  for (int i = threadIdx.x; i < nch * 64; i += GR_THREADS) reinterpret_cast<uint64_t*>(&tab[0][0])[i] = 0;
+  // every row is cleared, so the scan below reads and writes all GR_MAXCH rows without a
+  // bounds test (a test per read would make each read wait for the one before it)
+#pragma unroll
+  for (int i = threadIdx.x; i < GR_MAXCH * 64; i += GR_THREADS) reinterpret_cast<uint64_t*>(&tab[0][0])[i] = 0;
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < NKEY; ++j) {
@@ -79,30 +83,40 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
     }
   }
   __syncthreads();
-  // phase 2: per-expert exclusive scan over chunks, four threads per expert (chunks
-  // 16 q .. 16 q + 15 each, read at once), combined across the four lanes; totals
+  // phase 2: per-expert exclusive scan over chunks.  Wave w takes quarter q = w / 4 of the
+  // chunks (16 q .. 16 q + 15) for the 64 experts 64 (w % 4) ..: each of its reads is one
+  // contiguous table row (no bank conflicts), the quarter is skipped as a whole when it lies
+  // past nch, and the four quarters of an expert are combined through s_part
   {
-    static_assert(GR_THREADS == 4 * 256 && GR_MAXCH == 4 * 16, "four scan threads per expert");
-    const int e = threadIdx.x >> 2, q = threadIdx.x & 3;
+    static_assert(GR_THREADS == 4 * 256 && GR_MAXCH == 4 * 16, "four chunk quarters of 256 experts");
+    __shared__ int s_part[4][256];
+    const int e = threadIdx.x & 255, q = threadIdx.x >> 8;
+    const bool any = 16 * q < nch;  // the same for the whole wave
     int v[16], loc = 0;
+    if (any) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) v[t] = 16 * q + t < nch ? (int)tab[16 * q + t][e] : 0;
+      for (int t = 0; t < 16; ++t) v[t] = tab[16 * q + t][e];  // rows past nch hold zeros
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int c = v[t];
-      v[t] = loc;
-      loc += c;
+      for (int t = 0; t < 16; ++t) {
+        const int c = v[t];
+        v[t] = loc;
+        loc += c;
+      }
     }
-    int inc = loc;
-    int u = __shfl_up(inc, 1, 4);
-    if (q >= 1) inc += u;
-    u = __shfl_up(inc, 2, 4);
-    if (q >= 2) inc += u;
-    const int base = inc - loc;
+    s_part[q][e] = loc;
+    __syncthreads();
+    int base = 0, tot = 0;
 #pragma unroll
-    for (int t = 0; t < 16; ++t)
-      if (16 * q + t < nch) tab[16 * q + t][e] = (uint16_t)(v[t] + base);
-    if (q == 3) s_tot[e] = inc;
+    for (int qq = 0; qq < 4; ++qq) {
+      const int p = s_part[qq][e];
+      base += qq < q ? p : 0;
+      tot += p;
+    }
+    if (any) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) tab[16 * q + t][e] = (uint16_t)(v[t] + base);  // rows past nch unused
+    }
+    if (q == 0) s_tot[e] = tot;
   }
   __syncthreads();
   int total = 0;
@@ -137,10 +151,12 @@ DEV void group_block(const Ld& ld, int n, int E, int* __restrict__ counts, int* 
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < NKEY; ++j) {
+    // c < GR_MAXCH and i < GR_MAXN for every j, so the LDS reads need no bounds test and all
+    // of them are issued before the first store; pairs past n are not stored
     const int c = wave + GR_WAVES * (j >> 1), i = c * GR_CHUNK + (j & 1) * 64 + lane;
+    const int e = (int)keys[j];
+    const int slot = s_off[e] + (int)tab[c][e] + (int)rank[i];
     if (i < n) {
-      const int e = (int)keys[j];
-      const int slot = s_off[e] + (int)tab[c][e] + (int)rank[i];
       slot_of[i] = slot;
       if (row_of_slot) row_of_slot[slot] = i / topk;
     }

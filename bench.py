@@ -384,32 +384,34 @@ def main():
             # where the host sets it (one GPU's share of the GPU box's host is 16 cores)
             avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
             threads = min(avail, int(os.environ.get("OMP_NUM_THREADS", avail)))
+            hl0 = dict(hl, router=h["router"].view(np.uint16), nw=h["nw"])
+
+            def cpu_sample(nthreads, min_runs, budget_s):
+                """median us of one layer over >= min_runs runs (after 3 warm-ups) within budget_s"""
+                O.lib().or_set_threads(nthreads)
+                xs = x0.copy()
+                for _ in range(3):
+                    _, _, xs = O.cpu_layer_f32(hl0, xs, xs, H, I, TOPK)
+                ts, t_all = [], time.perf_counter()
+                while len(ts) < min_runs or (time.perf_counter() - t_all < budget_s and len(ts) < 2000):
+                    t1 = time.perf_counter()
+                    _, _, xs = O.cpu_layer_f32(hl0, xs, xs, H, I, TOPK)
+                    ts.append(time.perf_counter() - t1)
+                return float(np.median(ts)) * 1e6, len(ts), time.perf_counter() - t_all
+
+            us_all, n_all, s_all = cpu_sample(threads, 20, args.cpu_seconds)
+            us_one, n_one, s_one = cpu_sample(1, 20, args.cpu_seconds / 3)
             O.lib().or_set_threads(threads)
-            xs = x0
-            n, t_cpu = 0, 0.0
-            while t_cpu < args.cpu_seconds and n < 5000:
-                t1 = time.perf_counter()
-                _, ri, rw, rs = O.router_topk(h["router"].view(np.uint16), xs, h["nw"], 1e-6, E, TOPK)
-                _, xs = O.moe_decode(hl, xs, ri, rw, rs, xs, H, I, TOPK, nw=h["nw"], eps=1e-6)
-                t_cpu += time.perf_counter() - t1
-                n += 1
-            # the same layer on one thread (a shorter sample), for the per-core figure
-            O.lib().or_set_threads(1)
-            n1, t1s = 0, 0.0
-            while t1s < args.cpu_seconds / 3 and n1 < 2000:
-                t1 = time.perf_counter()
-                _, ri, rw, rs = O.router_topk(h["router"].view(np.uint16), xs, h["nw"], 1e-6, E, TOPK)
-                _, xs = O.moe_decode(hl, xs, ri, rw, rs, xs, H, I, TOPK, nw=h["nw"], eps=1e-6)
-                t1s += time.perf_counter() - t1
-                n1 += 1
-            O.lib().or_set_threads(threads)
-            cpu = {"value": round(t_cpu / n * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            cpu = {"value": round(us_all, 1), "unit": "us/layer", "cores": threads, "kind": "port",
                    "cores_note": f"all {threads} cores available to this process (affinity {avail}, "
                                  f"OMP_NUM_THREADS {os.environ.get('OMP_NUM_THREADS', 'unset')})",
-                   "sample": f"{n} decode layers (router + 8 int4 experts + int8 shared, fp64 accumulation) of layer 0, "
-                             f"{t_cpu:.1f} s",
-                   "value_1thread": round(t1s / n1 * 1e6, 1),
-                   "sample_1thread": f"{n1} decode layers on 1 thread, {t1s:.1f} s"}
+                   "sample": f"median of {n_all} decode layers of layer 0 (router + top-8 of 256 int4 experts + int8 "
+                             f"shared; every weight dequantised to fp32, fp32 dots, OpenMP over output rows; "
+                             f"oracle/cpu_baseline.c) after 3 warm-ups, {s_all:.1f} s",
+                   "value_1thread": round(us_one, 1),
+                   "sample_1thread": f"median of {n_one} layers on 1 thread, {s_one:.1f} s",
+                   "ms_per_40_layer_step": round(us_all * nl / 1000.0, 2),
+                   "gbs": round(bytes_layer / (us_all * 1e-6) / 1e9, 1)}
         except Exception as e:
             cpu = {"error": repr(e)}
 

@@ -230,13 +230,15 @@ class MoeStack:
         if int(self.sync[1].item()) != 0:
             raise dramamoe.DramaMoeError("dr_moe_decode_step timed out waiting for its workgroups")
 
-    def prefill(self, l: int, x, hn, chunk: int = 1024, stream=None) -> None:
+    def prefill(self, l: int, x, hn, chunk: int = 1024, stream=None, keep: dict | None = None) -> None:
         """Prefill of loaded layer l for rows token rows (the engine's moe_prefill,
         src/engine.rs:544-604): x f32 [rows, H] residual stream updated in place, hn bf16
         [rows, H] its RMSNorm.  Rows go in chunks of at most `chunk` (grouping handles up to
         8192 (row, expert) pairs per call): router GEMM, top-k, device-side grouping, gather,
         grouped expert GEMMs and the weighted combine, with the shared expert on a second stream
-        beside them; no host round trip."""
+        beside them; no host round trip.  With ``keep`` (a dict), the last chunk's routing
+        (idx, wts, sgate), grouping (slot_of) and bf16 activations (act in grouped-slot order,
+        sact per row) are left in it for inspection."""
         import torch
 
         P = dramamoe.ptr
@@ -290,6 +292,9 @@ class MoeStack:
             if overlap:
                 main.wait_event(join)
             lib.dr_moe_combine(P(xr), P(yp), P(slot_of), P(wts), P(sg), P(sh), n, k, H, st)
+        if keep is not None:
+            keep.update({"idx": idx[:n * k], "wts": wts[:n * k], "sgate": sg[:n], "slot_of": slot_of[:n * k],
+                         "act": act[:n * k * I], "sact": sact[:n * I]})
 
     def chain(self, x, stream=None) -> None:
         """The same layers through the engine's per-layer launches (router, then decode)."""

@@ -21,6 +21,7 @@ constexpr int WAVE = 64;
 // Codes (the header's DR_ERR_STEP_TIMEOUT / DR_ERR_PREFILL_WAIT / DR_ERR_ROUTE_WAIT).
 constexpr uint32_t kErrStepTimeout = 9001, kErrPrefillWait = 9002, kErrRouteWait = 9003;
 uint32_t* err_word();
+uint32_t* err_word_noalloc();  // the address if already set up (at library load), else nullptr; never allocates
 uint32_t err_pending();
 
 DEV void raise_err(uint32_t* err, uint32_t code) {

@@ -28,7 +28,18 @@ void err_setup() {
     return;
   }
   g_err_host = static_cast<uint32_t*>(p);
-  g_err_dev = static_cast<uint32_t*>(d);
+  __atomic_store_n(&g_err_dev, static_cast<uint32_t*>(d), __ATOMIC_RELEASE);
+}
+// Set up when the library is loaded, if the process sees a device, so that no launcher has to
+// allocate (the no-allocation step entry point only reads the word's address); a process that
+// loads the library before its device is visible sets it up on the first call of err_word().
+__attribute__((constructor)) void err_setup_at_load() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return;
+  }
+  std::call_once(g_err_once, err_setup);
 }
 }  // namespace
 
@@ -36,6 +47,7 @@ uint32_t* drm::err_word() {
   std::call_once(g_err_once, err_setup);
   return g_err_dev;
 }
+uint32_t* drm::err_word_noalloc() { return __atomic_load_n(&g_err_dev, __ATOMIC_ACQUIRE); }
 uint32_t drm::err_pending() {
   return g_err_host ? __atomic_load_n(g_err_host, __ATOMIC_ACQUIRE) : 0u;
 }

@@ -10,12 +10,13 @@
 // CU, 8 waves each) stay resident for the whole step and hand data to each other through
 // three all-to-all exchanges per layer: the 257 router logits, the 9 x 512 activations and
 // the 2048-float residual stream.  Each exchange is a "low latency" slot array: every value
-// travels in a 64-bit word with a tag (fp32 bits + 32-bit tag; the routed activations two
-// 24-bit floats + 16-bit tag, which halves the largest exchange), written with one cache-bypassing
+// travels in a 64-bit word with a tag (fp32 bits + 32-bit tag; by default the routed
+// activations two fp32 per word, each rounded to 21 mantissa bits with a 2-bit phase in its
+// two low mantissa bits, which halves the largest exchange), written with one cache-bypassing
 // (device-scope) store and read with device-scope loads until every word carries the tag of
-// the current phase.  A 64-bit access is single-copy atomic, so a reader never sees a value
-// without its tag and no separate flag, fence or counter is needed: one memory hop per
-// exchange.  Tags are epoch * 4096 + 3 layer + phase + 1, with the epoch read from sync[0] at
+// the current phase.  A 64-bit access is single-copy atomic (and each 32-bit half of a packed
+// activation word carries its own phase), so a reader never sees a value without its tag and
+// no separate flag, fence or counter is needed: one memory hop per exchange.  Tags are epoch * 4096 + 3 layer + phase + 1, with the epoch read from sync[0] at
 // launch and advanced by the launch's last act, so slots never need clearing between calls.
 //
 // Work map (g = global wave, 0..2047): router row g/8 on wave 0 of every block (row 256, the
@@ -754,10 +755,12 @@ std::atomic<int> g_act_bits{30};
 
 template <class F, class SH, bool A32>
 int launch_step_as(const dr_decode_layer* layers, int L, float* x, int E, float eps, uint64_t* ll, uint32_t* sync,
-                   int* idx_out, float* wts_out, float* sgate_out, float* xs_out, hipStream_t st) {
+                   int* idx_out, float* wts_out, float* sgate_out, float* xs_out, hipStream_t st, bool noalloc) {
   const void* k = reinterpret_cast<const void*>(&k_decode_step<F, SH, A32>);
   if (!step_grid_ok(k)) return -1;
-  uint32_t* err = err_word();
+  // the no-allocation entry point only reads the error word's address (set up when the library
+  // was loaded); the others set it up on first use
+  uint32_t* err = noalloc ? err_word_noalloc() : err_word();
   if (err_pending() == DR_ERR_STEP_TIMEOUT) return DR_ERR_STEP_TIMEOUT;  // until dr_last_error clears it
   hipLaunchKernelGGL((k_decode_step<F, SH, A32>), dim3(ST_NB), dim3(ST_NT), 0, st, layers, L, x, E, eps, ll, sync,
                      idx_out, wts_out, sgate_out, xs_out, err, g_wait_ticks.load(std::memory_order_relaxed));
@@ -767,12 +770,13 @@ int launch_step_as(const dr_decode_layer* layers, int L, float* x, int E, float 
 template <class F, class SH>
 int launch_step(const dr_decode_layer* layers, int L, float* x, int E, int H, int I, int topk, float eps,
                 uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out, float* xs_out,
-                hipStream_t st) {
+                hipStream_t st, bool noalloc = false) {
   if (H != ST_H || I != ST_I || topk != ST_TOPK || E < ST_TOPK || E > ST_MAXE || L < 1 || L > ST_MAXL) return -1;
   if (!layers || !x || !ll || !sync) return -1;
   if (g_act_bits.load(std::memory_order_relaxed) == 30)
-    return launch_step_as<F, SH, false>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
-  return launch_step_as<F, SH, true>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st);
+    return launch_step_as<F, SH, false>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st,
+                                        noalloc);
+  return launch_step_as<F, SH, true>(layers, L, x, E, eps, ll, sync, idx_out, wts_out, sgate_out, xs_out, st, noalloc);
 }
 
 constexpr int ST_SCRATCH_WORDS = LL_WORDS + 2;  // ll, then sync[4] as two 64-bit words
@@ -824,7 +828,7 @@ API int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_la
   hipLaunchKernelGGL(k_zero_scratch, dim3(28), dim3(256), 0, (hipStream_t)st, p, ST_SCRATCH_WORDS);
   return launch_step<StepQ4<ScaleBF16>, Q8RowBF16>(layers, n_layers, x, E, H, I, topk, eps, p,
                                                    reinterpret_cast<uint32_t*>(p + LL_WORDS), idx_out, wts_out,
-                                                   sgate_out, xs_out, (hipStream_t)st);
+                                                   sgate_out, xs_out, (hipStream_t)st, true);
 }
 
 API int dr_step_set_act_exchange(int bits) {

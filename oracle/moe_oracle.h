@@ -88,6 +88,9 @@ typedef struct {
   int sh_group_d;  /* group along K = I for shared down (128 or I) */
 } or_moe_weights;
 
+/* fp32 host baseline of one int4 decode layer (cpu_baseline.c; bench.py's cpu_baseline leg) */
+int or_cpu_layer_f32(const or_moe_weights* w, const uint16_t* router, const float* nw, float eps, const float* x,
+                     const float* res, float* y, int E, int H, int I, int topk, int* idx, float* wts);
 int or_moe_decode(const or_moe_weights* w, const float* x, const int* idx, const float* wts,
                   const float* sgate, const float* res, float* act, float* y, int H, int I, int topk,
                   const float* nw, float eps);

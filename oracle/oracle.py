@@ -66,6 +66,7 @@ def _declare(L: C.CDLL) -> None:
         "or_moe_prefill_layer": (i, [P, P, i, P, P, P, P, i, i, i]),
         "or_moe_prefill_experts": (i, [P, P, P, P, i, P, P, i, i]),
         "or_shared_prefill": (i, [P, P, i, P, P, i, i]),
+        "or_cpu_layer_f32": (i, [P, P, P, f, P, P, P, i, i, i, i, P, P]),
         "or_num_threads": (i, []),
         "or_set_threads": (None, [i]),
     }
@@ -259,6 +260,24 @@ def moe_decode(layer, x, idx, wts, sgate, res, H, I, topk, nw=None, eps=1e-6):
     if rc:
         raise ValueError("or_moe_decode failed")
     return act, y
+
+
+def cpu_layer_f32(layer, x, res, H, I, topk, eps=1e-6):
+    """fp32 host baseline of one int4 decode layer (router, top-k, experts, shared): returns
+    (idx, wts, y).  Measurement infrastructure, checked against moe_decode by the tests."""
+    w, keep = moe_weights(layer)
+    E = layer["gu_q"].shape[0]
+    x = np.ascontiguousarray(x, np.float32)
+    res = np.ascontiguousarray(res, np.float32)
+    y = np.empty(H, np.float32)
+    idx = np.empty(topk, np.int32)
+    wts = np.empty(topk, np.float32)
+    nw = layer.get("nw")
+    rc = lib().or_cpu_layer_f32(C.byref(w), ptr(np.ascontiguousarray(layer["router"])), ptr(nw) if nw is not None else None,
+                                eps, ptr(x), ptr(res), ptr(y), E, H, I, topk, ptr(idx), ptr(wts))
+    if rc:
+        raise ValueError("or_cpu_layer_f32: unsupported shape")
+    return idx, wts, y
 
 
 def moe_prefill_experts(layer, xp, offsets, counts, E, H, I):

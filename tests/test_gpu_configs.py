@@ -179,6 +179,55 @@ def test_cfg3_forty_layer_step_full_size():
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("fmt,act_bits", [("cfg", 30), ("ref", 32)])
+def test_cfg5_fp8_fused_step_full_size(fmt, act_bits):
+    """Configuration 5 batch 1 through the fused step (dr_moe_decode_step_fp8*): three layers of
+    256 block-FP8 experts, routing of every layer bit-exact against the oracle's router on the
+    step's own layer input, every layer output within 1e-3 + 1e-3 |ref|; act_bits is the routed
+    activations' transport between workgroups (30: the default, two fp32 per exchange word;
+    32: full fp32 as the reference's act buffer)."""
+    import torch
+
+    nl = 3
+    print(f"cfg5 fused fp8 step fmt={fmt} act exchange {act_bits}: generating {nl} layers", flush=True)
+    layers = [fp8_layer_gpu(90 + l + 10 * (fmt == "ref"), fmt) for l in range(nl)]
+    table = torch.tensor([[Lr[k].data_ptr() for k in KEYS] for Lr in layers], dtype=torch.int64, device="cuda")
+    ll = torch.zeros(D.STEP_LL_WORDS, dtype=torch.int64, device="cuda")
+    sync = torch.zeros(4, dtype=torch.int32, device="cuda")
+    idx = torch.full((nl * TOPK,), -1, dtype=torch.int32, device="cuda")
+    wts = torch.zeros(nl * TOPK, device="cuda")
+    sg = torch.zeros(nl, device="cuda")
+    xs = torch.zeros(nl * H, device="cuda")
+    x0 = np.random.default_rng(93).normal(0, 1, H).astype(np.float32)
+    xd = dev(x0)
+    lib, P = D.lib(), D.ptr
+    torch.cuda.synchronize()
+    fn = lib.dr_moe_decode_step_fp8_bf16s if fmt == "cfg" else lib.dr_moe_decode_step_fp8
+    lib.dr_step_set_act_exchange(act_bits)
+    try:
+        fn(P(table), nl, P(xd), E, H, I, TOPK, 1e-6, P(ll), P(sync), P(idx), P(wts), P(sg), P(xs), D.stream_ptr())
+        torch.cuda.synchronize()
+    finally:
+        lib.dr_step_set_act_exchange(0)
+    assert int(host(sync)[1]) == 0
+    gi, gw, gs = host(idx).reshape(nl, TOPK), host(wts).reshape(nl, TOPK), host(sg)
+    xsh = host(xs).reshape(nl, H)
+    np.testing.assert_array_equal(bits(host(xd)), bits(xsh[-1]))
+    for l in range(nl):
+        xin = x0 if l == 0 else xsh[l - 1]
+        rh, nwh = layers[l]["router"].cpu().numpy().view(np.uint16), layers[l]["nw"].cpu().numpy()
+        _, ri, rw, rs = O.router_topk(rh, xin, nwh, 1e-6, E, TOPK)
+        np.testing.assert_array_equal(gi[l], ri, err_msg=f"layer {l} experts")
+        np.testing.assert_array_equal(bits(gw[l]), bits(rw), err_msg=f"layer {l} weights")
+        assert bits(gs[l:l + 1])[0] == bits(np.float32(rs)), f"layer {l} shared gate"
+        used, ric = compact(ri)
+        hl = host_layer(layers[l], "fp8", fmt, used)
+        _, ry = O.moe_decode(hl, xin, ric, rw, rs, xin, H, I, TOPK, nw=nwh, eps=1e-6)
+        assert_close(xsh[l], ry, what=f"layer {l} output")
+    del layers, table
+    torch.cuda.empty_cache()
+
+
 # ---------------------------------------------------------------------------------------------
 # prefill-path layer chains (configuration 5 batch 4, configuration 4 skewed)
 # ---------------------------------------------------------------------------------------------
@@ -223,35 +272,45 @@ def run_chain(Ld, kind, fmt, hn, x0, routing=None):
 def check_chain(Ld, kind, fmt, hn, x0, g, ri, rw, rs):
     """Grouping exact; layer output within 1e-3 + 1e-3 |ref| plus the propagation of the bf16
     act rounding flips observed (the bar of the 300-row layer test in test_gpu_prefill.py)."""
-    rows = hn.shape[0]
-    n = rows * TOPK
     rc, ro, rso = O.moe_group(ri, E)
     np.testing.assert_array_equal(g["counts"], rc)
     np.testing.assert_array_equal(g["slot_of"], rso)
     used, ric = compact(ri)
+    np.testing.assert_array_equal(O.moe_group(ric, used.size)[2], rso)  # renumbering keeps the slot order
     Lh = host_layer(Ld, kind, fmt, used)
-    ref = O.moe_prefill_layer(Lh, hn, rows, ric, rw, rs, x0, H, I, TOPK).astype(np.float64)
-    cc, co, cso = O.moe_group(ric, used.size)
-    np.testing.assert_array_equal(cso, rso)  # renumbering keeps the slot order
-    xpr = np.empty((n, H), np.uint16)
+    check_layer_with_flips(Lh, hn, x0, g["act"], g["sact"], g["x"], ric, rw, rs)
+
+
+def check_layer_with_flips(Lh, hn, x0, act, sact, xgot, ric, rw, rs):
+    """Prefill layer output xgot against O.moe_prefill_layer: |gpu - ref| <= 1e-3 + 1e-3 |ref|
+    plus exactly the propagation of the bf16 act rounding flips observed between the GPU's
+    routed / shared activations (act, sact: bf16 bits in grouped-slot / row order) and the
+    oracle's.  Lh holds only the experts the routing uses, ric the routing renumbered into them."""
+    rows = hn.shape[0]
+    n = rows * TOPK
+    ne = Lh["gu_q"].shape[0]
+    Hh, Ih = Lh["H"], Lh["I"]
+    ref = O.moe_prefill_layer(Lh, hn, rows, ric, rw, rs, x0, Hh, Ih, TOPK).astype(np.float64)
+    cc, co, cso = O.moe_group(ric, ne)
+    xpr = np.empty((n, Hh), np.uint16)
     xpr[cso] = hn[np.arange(n) // TOPK]
-    ract, _ = O.moe_prefill_experts(Lh, xpr, co, cc, used.size, H, I)
-    rsact, _ = O.shared_prefill(Lh, hn, rows, H, I)
-    af, rf = check_act(g["act"], ract, "routed act")
-    saf, srf = check_act(g["sact"], rsact, "shared act")
-    extra_slot = np.zeros((n, H))
-    for e in range(used.size):
+    ract, _ = O.moe_prefill_experts(Lh, xpr, co, cc, ne, Hh, Ih)
+    rsact, _ = O.shared_prefill(Lh, hn, rows, Hh, Ih)
+    af, rf = check_act(act, ract, "routed act")
+    saf, srf = check_act(sact, rsact, "shared act")
+    extra_slot = np.zeros((n, Hh))
+    for e in range(ne):
         sl = slice(co[e], co[e] + cc[e])
         d = np.abs(af[sl] - rf[sl])
         if d.any():
             extra_slot[sl] = d @ np.abs(expert_dense(Lh, "d", e).astype(np.float64)).T
-    sd = O.dequant_q8(Lh["sd_q"], Lh["sd_s"], Lh["sh_kind"], Lh["sh_group_d"], H, I).astype(np.float64)
+    sd = O.dequant_q8(Lh["sd_q"], Lh["sd_s"], Lh["sh_kind"], Lh["sh_group_d"], Hh, Ih).astype(np.float64)
     sig = 1 / (1 + np.exp(-np.asarray(rs, np.float64)))
     extra = sig[:, None] * (np.abs(saf - srf) @ np.abs(sd).T)
-    extra += np.einsum("rk,rkc->rc", np.asarray(rw, np.float64).reshape(rows, TOPK), extra_slot[rso.reshape(rows, TOPK)])
-    got = g["x"].astype(np.float64)
+    extra += np.einsum("rk,rkc->rc", np.asarray(rw, np.float64).reshape(rows, TOPK), extra_slot[cso.reshape(rows, TOPK)])
+    got = np.asarray(xgot, np.float64).reshape(rows, Hh)
     bad = np.abs(got - ref) > 1e-3 + 1e-3 * np.abs(ref) + extra
-    print(f"experts hit {used.size}, act flips routed {int((af != rf).sum())}, shared {int((saf != srf).sum())}, "
+    print(f"experts hit {ne}, act flips routed {int((af != rf).sum())}, shared {int((saf != srf).sum())}, "
           f"max |err| {np.abs(got - ref).max():.2e}", flush=True)
     assert not bad.any(), f"layer output: {int(bad.sum())} outside tolerance + flip propagation"
 

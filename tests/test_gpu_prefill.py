@@ -461,3 +461,37 @@ def test_reference_shared_expert_sequence_300_rows():
     ref_act = hh[:, :I] / (1 + np.exp(-hh[:, :I])) * hh[:, I:]
     af, rf = check_act(g_act, synth.f32_to_bf16(ref_act.astype(np.float32)), "shared act (reference sequence)")
     assert_close_with_flips(g_out, rf @ wdf.T, wdf, af, rf, "shared out (reference sequence)")
+
+
+@pytest.mark.parametrize("rows,E,skew", [(300, 256, False), (300, 256, True), (1024, 256, True), (4, 256, False),
+                                         (1, 8, False), (37, 64, True)])
+def test_group_rows_matches_oracle(rows, E, skew):
+    """dr_moe_group_rows (grouping of a routing given from outside, as bench.py's skewed
+    configuration 4 uses): counts, offsets and slot_of equal to the oracle's stable grouping of
+    the rows * 8 pairs, row_of_slot the inverse map; skewed: 10% of the experts take about half
+    of the pairs (the reference's semantics: kernels/drama.cu:744-778, src/engine.rs:564-575)."""
+    topk = 8
+    rng = np.random.default_rng(rows + E + 17 * skew)
+    idx = np.empty((rows, topk), np.int32)
+    hot = rng.choice(E, max(1, E // 10), replace=False)
+    for r in range(rows):  # distinct experts per row, as a router produces
+        nh = int(rng.binomial(topk, 0.5)) if skew else 0
+        nh = min(nh, hot.size)
+        hsel = rng.choice(hot, nh, replace=False)
+        rest = rng.choice(np.setdiff1d(np.arange(E), hsel), topk - nh, replace=False)
+        idx[r] = rng.permutation(np.concatenate([hsel, rest]))
+    idx = idx.ravel()
+    n = rows * topk
+    rc, ro, rso = O.moe_group(idx, E)
+    if skew and E == 256:
+        assert rc[hot].sum() >= 0.4 * n, "routing is not skewed as intended"
+    counts, offsets, slot_of, row_of_slot = t_i32(E), t_i32(E), t_i32(n), t_i32(n + 16)
+    for rep in range(2):  # outputs are fully rewritten by every call
+        counts.fill_(-7)
+        slot_of.fill_(-7)
+        D.lib().dr_moe_group_rows(D.ptr(dev(idx)), rows, topk, E, D.ptr(counts), D.ptr(offsets), D.ptr(slot_of),
+                                  D.ptr(row_of_slot), D.stream_ptr())
+        np.testing.assert_array_equal(host(counts), rc)
+        np.testing.assert_array_equal(host(offsets), ro)
+        np.testing.assert_array_equal(host(slot_of), rso)
+        np.testing.assert_array_equal(host(row_of_slot)[rso], np.arange(n) // topk)

@@ -161,6 +161,29 @@ def test_cfg5_fp8_batch4_rows_path_full_size(fmt):
     torch.cuda.empty_cache()
 
 
+def _check_rows_vs_oracle(Ld, fmt, E, x, out):
+    """Routed launch outputs of one call against the oracle, row by row: logits, picks, weights
+    and shared gate bit for bit with O.router_topk on that row, y (x + layer, res aliasing x)
+    within 1e-3 + 1e-3 |ref| of O.moe_decode over the experts the row picked."""
+    from test_gpu_configs import compact, host_layer
+
+    lg, idx, wts, sg, _, y, _ = out
+    rows = x.shape[0]
+    router = Ld["router"].cpu().numpy().view(np.uint16)
+    nw = Ld["nw"].cpu().numpy()
+    gl, gi, gw, gy = lg.reshape(rows, E + 1), idx.reshape(rows, TOPK), wts.reshape(rows, TOPK), y.reshape(rows, H)
+    for r in range(rows):
+        rl, ri, rw, rs = O.router_topk(router, x[r], nw, 1e-6, E, TOPK)
+        np.testing.assert_array_equal(bits(gl[r]), bits(rl), err_msg=f"row {r} logits")
+        np.testing.assert_array_equal(gi[r], ri, err_msg=f"row {r} experts")
+        np.testing.assert_array_equal(bits(gw[r]), bits(rw), err_msg=f"row {r} weights")
+        assert bits(sg[r:r + 1])[0] == bits(np.float32(rs)), f"row {r} shared gate"
+        used, ric = compact(ri)
+        hl = host_layer(Ld, "fp8", fmt, used)
+        _, ry = O.moe_decode(hl, x[r], ric, rw, rs, x[r], H, I, TOPK, nw=nw, eps=1e-6)
+        assert_close(gy[r], ry, what=f"routed launch row {r}")
+
+
 @pytest.mark.parametrize("fmt,rows,E", [("cfg", 4, 256), ("ref", 4, 256), ("cfg", 5, 256), ("cfg", 1, 256),
                                          ("cfg", 3, 256), ("cfg", 4, 64), ("cfg", 2, 9)])
 def test_routed_fp8_rows_equal_three_launch_path(fmt, rows, E):
@@ -169,7 +192,8 @@ def test_routed_fp8_rows_equal_three_launch_path(fmt, rows, E):
     dr_router_topk_rows + dr_moe_decode_rows_fp8(_bf16s) on the same inputs: logits, picks,
     weights, shared gates, activations and outputs bit for bit (both run the same arithmetic),
     over three calls in a row with different x on one counter and tag buffer (each launch tags
-    its picks afresh), the last with y aliasing x and res."""
+    its picks afresh), the last with y aliasing x and res.  The routed launch's first and last
+    calls are also checked against the oracle row by row (routing bit-exact, y in tolerance)."""
     import torch
 
     from test_gpu_configs import fp8_layer_gpu
@@ -213,6 +237,8 @@ def test_routed_fp8_rows_equal_three_launch_path(fmt, rows, E):
             torch.cuda.synchronize()
             assert L.dr_last_error() == 0
             outs.append([host(t) for t in (lg, idx, wts, sg, act, y, yb)])
+            if fused and call != 1:
+                _check_rows_vs_oracle(Ld, fmt, E, x, outs[-1])
         for name, a, b in zip(("logits", "idx", "wts", "sgate", "act", "y", "yb"), *outs):
             np.testing.assert_array_equal(bits(a) if a.dtype == np.float32 else a,
                                           bits(b) if b.dtype == np.float32 else b, err_msg=f"call {call}: {name}")

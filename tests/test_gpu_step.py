@@ -273,11 +273,10 @@ def test_step_gives_up_loudly_when_a_previous_call_timed_out():
         _clear_library_error()
 
 
-def test_step_beside_a_busy_stream_is_correct_or_reports():
-    """Matrix products queued on a second stream hold CUs while the step launches, so its 256
-    workgroups may not all be resident at once.  With a 2 ms wait limit the step must either
-    give the oracle's bits or report DR_ERR_STEP_TIMEOUT with a NaN x; every kernel exits by
-    itself (the step's waits are bounded)."""
+def _busy_stream_step(limit_us):
+    """The fused step launched while 40 4096^3 bf16 matrix products queued on a second stream
+    hold CUs, so the step's 256 workgroups may not all be resident at once.  Returns the
+    dr_stream_sync code, the stack, x0 and the step's outputs."""
     import torch
 
     L = D.lib()
@@ -289,7 +288,8 @@ def test_step_beside_a_busy_stream_is_correct_or_reports():
     _clear_library_error()
     side = torch.cuda.Stream()
     try:
-        L.dr_step_set_wait_limit(2000)
+        if limit_us:
+            L.dr_step_set_wait_limit(limit_us)
         with torch.cuda.stream(side):
             for _ in range(40):
                 a = (a @ a) * 1e-3
@@ -304,15 +304,39 @@ def test_step_beside_a_busy_stream_is_correct_or_reports():
         assert rc == 0
         code = L.raw("dr_stream_sync")(main.cuda_stream)
         side.synchronize()
-        if code == 0:
-            print("step ran beside the busy stream and completed", flush=True)
-            check_stack(st, x0, host(idx).reshape(2, TOPK), host(wts).reshape(2, TOPK), host(sg),
-                        host(xs).reshape(2, H), host(xd))
-        else:
-            print("step gave up beside the busy stream (reported)", flush=True)
-            assert code == 9001
-            assert int(host(st.sync)[1]) == 1 and np.isnan(host(xd)).any()
+        out = (host(idx).reshape(2, TOPK), host(wts).reshape(2, TOPK), host(sg), host(xs).reshape(2, H), host(xd))
+        return code, st, x0, out
     finally:
         L.dr_step_set_wait_limit(0)
         torch.cuda.synchronize()
         _clear_library_error()
+
+
+def test_step_beside_a_busy_stream_completes_within_the_default_limit():
+    """With the default wait limit (0.2 s) the step's workgroups that could not start beside the
+    matrix products start as those drain (a few ms of work), so the step completes and gives the
+    oracle's bits: a concurrent workload that finishes within the limit only delays it."""
+    code, st, x0, (idx, wts, sg, xs, xf) = _busy_stream_step(0)
+    assert code == 0, f"step gave up beside a finite concurrent workload (code {code})"
+    assert int(host(st.sync)[1]) == 0
+    check_stack(st, x0, idx, wts, sg, xs, xf)
+
+
+def test_step_beside_a_busy_stream_is_correct_or_reports(record_property):
+    """With a 2 ms wait limit, shorter than the concurrent work, the step either completed (its
+    workgroups happened to be resident together) and gives the oracle's bits, or it reports
+    DR_ERR_STEP_TIMEOUT with sync[1] set and x holding NaN; which of the two happened is recorded
+    (the test property "outcome" and a warning on give-up).  Every kernel exits by itself."""
+    import warnings
+
+    code, st, x0, (idx, wts, sg, xs, xf) = _busy_stream_step(2000)
+    if code == 0:
+        record_property("outcome", "completed")
+        print("step ran beside the busy stream and completed", flush=True)
+        check_stack(st, x0, idx, wts, sg, xs, xf)
+    else:
+        record_property("outcome", "gave up (DR_ERR_STEP_TIMEOUT)")
+        warnings.warn("fused step beside a busy stream with a 2 ms wait limit gave up and reported "
+                      "DR_ERR_STEP_TIMEOUT (x poisoned with NaN)")
+        assert code == 9001
+        assert int(host(st.sync)[1]) == 1 and np.isnan(xf).any()

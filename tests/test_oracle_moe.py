@@ -174,3 +174,25 @@ def test_gemv_q4_and_q8_vs_numpy():
     q8, s8, kind, group = synth.q8_dense(rng, 64, 2048, "ref")
     np.testing.assert_allclose(O.gemv_q8(q8, s8, kind, group, x, 64, 2048),
                                np_dequant_q8(q8, s8, kind, group) @ x.astype(np.float64), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("fmt,E", [("cfg", 64), ("ref", 12)])
+def test_cpu_baseline_layer_matches_oracle(fmt, E):
+    """The fp32 host baseline bench.py times (or_cpu_layer_f32) computes the oracle's layer:
+    the same experts and weights (its own fp32 router agrees on these seeded inputs) and y
+    within 1e-3 + 1e-3 |ref| of or_moe_decode, on 1 and on several threads (same values)."""
+    L = synth.make_layer(31, E=E, fmt=fmt)
+    x = np.random.default_rng(32).normal(0, 1, H).astype(np.float32)
+    res = np.random.default_rng(33).normal(0, 1, H).astype(np.float32)
+    _, ri, rw, rs = O.router_topk(L["router"], x, L["nw"], 1e-6, E, 8)
+    _, ry = O.moe_decode(L, x, ri, rw, rs, res, H, I, 8, nw=L["nw"], eps=1e-6)
+    n0 = O.lib().or_num_threads()
+    try:
+        for th in (1, 4):
+            O.lib().or_set_threads(th)
+            idx, wts, y = O.cpu_layer_f32(L, x, res, H, I, 8)
+            np.testing.assert_array_equal(idx, ri)
+            np.testing.assert_allclose(wts, rw, rtol=1e-5, atol=1e-7)
+            assert np.all(np.abs(y.astype(np.float64) - ry) <= 1e-3 + 1e-3 * np.abs(ry))
+    finally:
+        O.lib().or_set_threads(n0)

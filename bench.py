@@ -83,6 +83,30 @@ def make_layer_gpu(gen, l):
 
     L["sgu_q"], L["sgu_s"] = q8(2 * I, H)
     L["sd_q"], L["sd_s"] = q8(H, I)
+    return pack_dense(L)
+
+
+DENSE_KEYS = ("router", "nw", "sgu_q", "sgu_s", "sd_q", "sd_s")
+
+
+def pack_dense(L):
+    """The layer's dense tensors (router, norm weight, shared expert) moved into one allocation,
+    each at a 256-byte aligned offset, as a loader that keeps a layer's small tensors together
+    lays them out: L["dense"] is that byte range, the range a preceding op warms (pf)."""
+    import torch
+
+    offs, o = [], 0
+    for k in DENSE_KEYS:
+        offs.append(o)
+        o += (L[k].numel() * L[k].element_size() + 255) & ~255
+    buf = torch.empty(o, dtype=torch.uint8, device="cuda")
+    for k, off in zip(DENSE_KEYS, offs):
+        t = L[k]
+        n = t.numel() * t.element_size()
+        v = buf[off:off + n].view(t.dtype).view(t.shape)
+        v.copy_(t)
+        L[k] = v
+    L["dense"] = buf
     return L
 
 
@@ -210,7 +234,7 @@ def main():
     def fused_step(outputs=False):
         rc = lib.dr_moe_decode_step_bf16s(P(table), nl, P(x), E, H, I, TOPK, 1e-6, P(ll), P(sync),
                                           P(s_idx) if outputs else None, P(s_wts) if outputs else None,
-                                          P(s_sg) if outputs else None, P(s_xs) if outputs else None, sp)
+                                          P(s_sg) if outputs else None, P(s_xs) if outputs else None, None, 0, sp)
         assert rc == 0
 
     def record_layer(L):
@@ -231,14 +255,72 @@ def main():
 
         def fused_one(i):
             rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * (i % nl), 1, P(x), E, H, I, TOPK, 1e-6, P(ll),
-                                              P(sync), None, None, None, None, sp)
+                                              P(sync), None, None, None, None, None, 0, sp)
             assert rc == 0
+        def fused_one_warm(i):  # the step warms the next layer's router, norm weight and shared expert
+            nxt = layers[(i + 1) % nl]["dense"]
+            rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * (i % nl), 1, P(x), E, H, I, TOPK, 1e-6, P(ll),
+                                              P(sync), None, None, None, None, P(nxt), nxt.numel(), sp)
+            assert rc == 0
+
         out = {}
-        for key, fn in (("fused_one_layer", fused_one), ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
+        for key, fn in (("fused_one_layer", fused_one), ("fused_one_layer_warm_next", fused_one_warm),
+                        ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
             ms = benchcfg.timed(fn, iters, st)
             out[key] = benchcfg.rec(ms * 1000, bytes_step // nl)
-        out["note"] = "one launch (fused) or three launches (chain) per layer, launch latency included"
+            out[key]["us_graph"] = round(benchcfg.timed_graph(fn, iters, st, nl) * 1000, 2)
+        out["note"] = ("one launch (fused) or three launches (chain) per layer, launch latency included; "
+                       "_warm_next: each step launch warms the next layer's dense block (router, norm weight, "
+                       "shared expert: pf/pf_bytes) during its last layer")
+        out["engine_sequence"] = engine_sequence(iters)
         return out
+
+    def engine_sequence(iters):
+        """The engine's decode order: an attention output projection (dr_gemv_q8, int8 2048 x 2048
+        with f16 scales per 128, its own weights per layer) before every MoE layer (the fused step
+        over that one layer), with and without the reference's prefetch chain (each op warms the
+        next op's weights: the projection the MoE layer's dense block, the MoE layer the next
+        projection).  moe_us = (projection + MoE) - projection alone, both per layer."""
+        import benchcfg
+
+        g = torch.Generator(device="cuda").manual_seed(77)
+        aw = [torch.randint(-127, 128, (H, H), generator=g, device="cuda", dtype=torch.int8) for _ in range(nl)]
+        asc = [((torch.rand(H, H // 128, generator=g, device="cuda") * 0.01 + 1e-4) / 127.0).to(torch.float16)
+               .view(torch.int16) for _ in range(nl)]
+        a_in = torch.randn(H, generator=g, device="cuda") * 0.1
+        torch.cuda.synchronize()
+
+        def proj(i, pf, pfb):
+            lib.dr_gemv_q8(P(aw[i]), P(asc[i]), P(a_in), P(x), P(x), H, H, None, 1e-6, pf, pfb, sp)
+
+        def moe(i, pf, pfb):
+            rc = lib.dr_moe_decode_step_bf16s(P(table) + 80 * i, 1, P(x), E, H, I, TOPK, 1e-6, P(ll), P(sync), None,
+                                              None, None, None, pf, pfb, sp)
+            assert rc == 0
+
+        def pair(i, warm):
+            i %= nl
+            d, a2 = layers[i]["dense"], aw[(i + 1) % nl]
+            proj(i, P(d) if warm else None, d.numel() if warm else 0)
+            moe(i, P(a2) if warm else None, a2.numel() if warm else 0)
+
+        def proj_only(i, warm):
+            i %= nl
+            a2 = aw[(i + 1) % nl]
+            proj(i, P(a2) if warm else None, a2.numel() if warm else 0)
+
+        res = {}
+        for warm in (False, True):
+            tag = "warm" if warm else "cold"
+            # replayed from HIP graphs of nl layers: no host launch gaps between the ops
+            both = benchcfg.timed_graph(lambda i: pair(i, warm), iters, st, nl) * 1000
+            alone = benchcfg.timed_graph(lambda i: proj_only(i, warm), iters, st, nl) * 1000
+            res[tag] = {"projection_plus_moe_us": round(both, 2), "projection_alone_us": round(alone, 2),
+                        "moe_us": round(both - alone, 2)}
+        res["note"] = ("engine order per layer: attention output projection then the MoE layer (one-layer fused "
+                       "step); warm = the prefetch chain on (pf/pf_bytes of both ops)")
+        del aw, asc
+        return res
 
     if args.profile_small:
         import benchcfg
@@ -441,8 +523,12 @@ def main():
         "fused_act32_note": "the same step with every routed activation exchanged as a full fp32 with a 32-bit "
                             "phase tag (dr_step_set_act_exchange(32)), as the reference's fp32 act buffer",
         "engine_one_layer_us": (extra or {}).get("cfg2_one_layer", {}).get("fused_one_layer", {}).get("us"),
+        "engine_one_layer_warm_us": (((extra or {}).get("cfg2_one_layer", {}).get("engine_sequence") or {})
+                                     .get("warm", {}).get("moe_us")),
         "engine_one_layer_note": "one MoE layer per launch (the engine interleaves attention between MoE "
-                                 "layers, so a drop-in caller launches the step with n_layers = 1)",
+                                 "layers, so a drop-in caller launches the step with n_layers = 1); _warm_us: the "
+                                 "same layer in the engine's order behind an attention projection with the "
+                                 "prefetch chain on (configs.cfg2_one_layer.engine_sequence)",
         "fused_graph_us_per_layer": round(fused_graph_ms * 1000.0 / nl, 3),
         "chain_eager_us_per_layer": None if args.profile else round(eager_ms * 1000.0 / nl, 3),
         "chain_graph_us_per_layer": None if args.profile else round(graph_ms * 1000.0 / nl, 3),

@@ -336,7 +336,7 @@ def config5_fp8(lib, st, iters=100, copies=4):
 
     def fused(i):
         lib.dr_moe_decode_step_fp8_bf16s(P(table), nl, P(x), E, H, I, TOPK, 1e-6, P(ll), P(sync), None, None, None,
-                                         None, sp)
+                                         None, None, 0, sp)
 
     msf = timed(fused, max(1, iters // 10), st)
     if int(sync[1].item()) != 0:

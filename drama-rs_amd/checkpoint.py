@@ -217,16 +217,30 @@ class MoeStack:
         key = int(st or 0)
         if key not in self._gemm:
             h = ctypes.c_void_p()
-            self.lib.dr_cublas_create(ctypes.byref(h), st)
+            self.lib.dr_cublas_create(ctypes.byref(h), st)  # raises DramaMoeError on a nonzero return
+            if not h.value:
+                raise dramamoe.DramaMoeError("dr_cublas_create returned a null handle")
             self._gemm[key] = h.value
         return self._gemm[key]
+
+    def close(self) -> None:
+        """Releases the GEMM handles created per stream (the tensors go with the object)."""
+        for h in self._gemm.values():
+            self.lib.dr_cublas_destroy(h)
+        self._gemm.clear()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def step(self, x, stream=None, idx_out=None, wts_out=None, sgate_out=None, xs_out=None) -> None:
         """x (f32 [H], device) through every loaded layer in one fused launch, in place."""
         P = dramamoe.ptr
         f = self.lib.dr_moe_decode_step_fp8 if self.fp8 else self.lib.dr_moe_decode_step
         f(P(self.table), len(self.layers), P(x), self.E, self.H, self.I, self.topk, self.eps, P(self.ll), P(self.sync),
-          P(idx_out), P(wts_out), P(sgate_out), P(xs_out), stream if stream is not None else dramamoe.stream_ptr())
+          P(idx_out), P(wts_out), P(sgate_out), P(xs_out), None, 0, stream if stream is not None else dramamoe.stream_ptr())
         if int(self.sync[1].item()) != 0:
             raise dramamoe.DramaMoeError("dr_moe_decode_step timed out waiting for its workgroups")
 

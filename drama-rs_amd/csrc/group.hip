@@ -221,12 +221,15 @@ __global__ void __launch_bounds__(GR_THREADS)
     }
     if (lane == 0) sgate[r] = lg[sub][E];
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  // hand-over to the last block: the block's idx stores happen before its count (workgroup
+  // barrier, then a release increment at agent scope); the block that sees the final count
+  // acquires it before any thread reads idx
   __syncthreads();
   if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
   if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   group_block([&](int i) { return __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
               rows * topk, E, counts, offsets, slot_of, 0, nullptr, row_of_slot, topk);
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -139,4 +139,8 @@ API int dr_cublas_create(void** h, hipStream_t s) {
   *h = g;
   return 0;
 }
+API int dr_cublas_destroy(void* h) {
+  delete static_cast<GemmHandle*>(h);
+  return 0;
+}
 hipStream_t gemm_handle_stream(void* h) { return h ? static_cast<GemmHandle*>(h)->st : nullptr; }

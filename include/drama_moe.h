@@ -172,6 +172,10 @@ int dr_gemv_bf16(const dr_bf16* w, const float* x, float* y, int n, int k, const
 /* Extensions: no counterpart in src/ffi.rs                                                */
 /* ===================================================================================== */
 
+/* Releases a handle of dr_cublas_create (NULL is a no-op).  The reference keeps its BLAS handle
+ * for the engine's lifetime and has no counterpart; for callers that create handles per stream. */
+int dr_cublas_destroy(void* h);
+
 /* Device-side grouping in one launch: counts (histogram), offsets (exclusive scan) and
  * slot_of (stable counting sort of the n pairs by expert), replacing dr_moe_count + the host
  * scan of src/engine.rs:564-575, so a prefill layer needs no host round trip.
@@ -349,20 +353,25 @@ typedef struct dr_decode_layer {
  *   ll        u64 [DR_STEP_LL_WORDS] exchange buffer, sync u32 [4]: both zeroed once by the
  *             caller before the first call and then left alone (a call advances sync[0]);
  *             sync[1] != 0 reports that a call timed out waiting for its workgroups: that call
- *             leaves x all NaN (blocks that gave up poison it) and raises DR_ERR_STEP_TIMEOUT,
+ *             leaves NaN in x (every block that gives up overwrites all of x with NaN; a block
+ *             that completed its last layer may still store its own rows afterwards) and raises
+ *             DR_ERR_STEP_TIMEOUT,
  *             which dr_stream_sync reports and dr_last_error returns and clears; until then the
  *             step launchers return DR_ERR_STEP_TIMEOUT, and calls made before the caller zeroes
  *             sync and ll again give up at once (NaN x, the error raised again);
  *   idx_out i32 [n_layers*8], wts_out f32 [n_layers*8], sgate_out f32 [n_layers],
- *   xs_out f32 [n_layers*h]: optional (NULL) per-layer routing and layer outputs.
+ *   xs_out f32 [n_layers*h]: optional (NULL) per-layer routing and layer outputs;
+ *   pf/pf_bytes: a range the step warms in the memory-side cache after its last layer (the
+ *             next op's weights, as dr_moe_decode's pf; the prefetch chain of
+ *             src/engine.rs:674-708), NULL / 0 for none.
  * Needs 256 co-resident workgroups of 512 threads (one MI355X); returns -1 otherwise.  Calls
  * sharing one ll/sync pair must be stream ordered. */
 int dr_moe_decode_step(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i, int topk,
                        float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
-                       float* xs_out, dr_stream_t st);
+                       float* xs_out, const char* pf, size_t pf_bytes, dr_stream_t st);
 int dr_moe_decode_step_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                              int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
-                             float* sgate_out, float* xs_out, dr_stream_t st);
+                             float* sgate_out, float* xs_out, const char* pf, size_t pf_bytes, dr_stream_t st);
 /* Transport of the routed activations between the fused step's workgroups, for later launches.
  * 30 (default; 0 restores it) packs two fp32 per slot with the exchange phase in the two low
  * mantissa bits of each: the activations reach the down projection rounded to 21 mantissa bits
@@ -386,10 +395,10 @@ int dr_step_set_wait_limit(uint32_t us);
  * (kernels/drama.cu:602-742), which these replace for a whole stack of layers. */
 int dr_moe_decode_step_fp8(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i, int topk,
                            float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out, float* sgate_out,
-                           float* xs_out, dr_stream_t st);
+                           float* xs_out, const char* pf, size_t pf_bytes, dr_stream_t st);
 int dr_moe_decode_step_fp8_bf16s(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                                  int topk, float eps, uint64_t* ll, uint32_t* sync, int* idx_out, float* wts_out,
-                                 float* sgate_out, float* xs_out, dr_stream_t st);
+                                 float* sgate_out, float* xs_out, const char* pf, size_t pf_bytes, dr_stream_t st);
 
 /* ===================================================================================== */
 /* Entry point that allocates nothing -- no counterpart in the reference.                 */
@@ -403,7 +412,7 @@ int dr_moe_decode_step_fp8_bf16s(const dr_decode_layer* layers, int n_layers, fl
  * Same shapes and limits as dr_moe_decode_step_bf16s (n_layers <= 1365, else -1). */
 int dr_moe_decode_step_bf16s_noalloc(const dr_decode_layer* layers, int n_layers, float* x, int e, int h, int i,
                                      int topk, float eps, int* idx_out, float* wts_out, float* sgate_out,
-                                     float* xs_out, dr_stream_t st);
+                                     float* xs_out, const char* pf, size_t pf_bytes, dr_stream_t st);
 
 #ifdef __cplusplus
 }

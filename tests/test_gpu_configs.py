@@ -137,7 +137,7 @@ def test_cfg3_forty_layer_step_full_size():
     torch.cuda.synchronize()
     print("cfg3: step launch", flush=True)
     lib.dr_moe_decode_step_bf16s(P(table), nl, P(xd), E, H, I, TOPK, 1e-6, P(ll), P(sync), P(idx), P(wts), P(sg),
-                                 P(xs), D.stream_ptr())
+                                 P(xs), None, 0, D.stream_ptr())
     torch.cuda.synchronize()
     assert int(host(sync)[1]) == 0
     gi, gw, gs = host(idx).reshape(nl, TOPK), host(wts).reshape(nl, TOPK), host(sg)
@@ -163,7 +163,7 @@ def test_cfg3_forty_layer_step_full_size():
     xg = torch.zeros(H, device="cuda")
     g = ctypes.c_void_p()
     lib.dr_graph_begin(sp)
-    lib.dr_moe_decode_step_bf16s(P(table), nl, P(xg), E, H, I, TOPK, 1e-6, P(ll), P(sync), None, None, None, None, sp)
+    lib.dr_moe_decode_step_bf16s(P(table), nl, P(xg), E, H, I, TOPK, 1e-6, P(ll), P(sync), None, None, None, None, None, 0, sp)
     lib.dr_graph_end(sp, ctypes.byref(g))
     try:
         for rep in range(3):
@@ -205,7 +205,7 @@ def test_cfg5_fp8_fused_step_full_size(fmt, act_bits):
     fn = lib.dr_moe_decode_step_fp8_bf16s if fmt == "cfg" else lib.dr_moe_decode_step_fp8
     lib.dr_step_set_act_exchange(act_bits)
     try:
-        fn(P(table), nl, P(xd), E, H, I, TOPK, 1e-6, P(ll), P(sync), P(idx), P(wts), P(sg), P(xs), D.stream_ptr())
+        fn(P(table), nl, P(xd), E, H, I, TOPK, 1e-6, P(ll), P(sync), P(idx), P(wts), P(sg), P(xs), None, 0, D.stream_ptr())
         torch.cuda.synchronize()
     finally:
         lib.dr_step_set_act_exchange(0)

@@ -45,7 +45,7 @@ class Stack:
         fn = getattr(D.lib(), name)
         fn(D.ptr(self.table), n, D.ptr(x_dev), self.E, H, I, TOPK, 1e-6, D.ptr(self.ll), D.ptr(self.sync),
            D.ptr(idx) if want_outputs else None, D.ptr(wts) if want_outputs else None,
-           D.ptr(sg) if want_outputs else None, D.ptr(xs) if want_outputs else None, D.stream_ptr())
+           D.ptr(sg) if want_outputs else None, D.ptr(xs) if want_outputs else None, None, 0, D.stream_ptr())
         torch.cuda.synchronize()
         return host(idx).reshape(n, TOPK), host(wts).reshape(n, TOPK), host(sg), host(xs).reshape(n, H)
 
@@ -104,7 +104,7 @@ def test_step_in_band_phase_over_launches_of_any_length():
             xs = torch.zeros(n * H, device="cuda")
             L.dr_moe_decode_step_bf16s(D.ptr(st.table) + 80 * first, n, D.ptr(xd), st.E, H, I, TOPK, 1e-6,
                                        D.ptr(st.ll), D.ptr(st.sync), D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(xs),
-                                       D.stream_ptr())
+                                       None, 0, D.stream_ptr())
             torch.cuda.synchronize()
             assert int(host(st.sync)[1]) == 0, "step reported a timeout"
 
@@ -193,7 +193,7 @@ def test_step_rejects_bad_shapes():
     x = dev(np.zeros(H, np.float32))
     L = D.lib()
     base = [D.ptr(st.table), 1, D.ptr(x), 16, H, I, TOPK, 1e-6, D.ptr(st.ll), D.ptr(st.sync), None, None, None, None,
-            D.stream_ptr()]
+            None, 0, D.stream_ptr()]
     for pos, bad in ((4, 1024), (5, 256), (6, 4), (3, 257), (3, 4), (1, 0), (1, 2000)):
         a = list(base)
         a[pos] = bad
@@ -220,7 +220,7 @@ def test_step_graph_replays_match_eager():
     g = ctypes.c_void_p()
     L.dr_graph_begin(sp)
     L.dr_moe_decode_step_bf16s(D.ptr(st.table), 2, D.ptr(xg), 64, H, I, TOPK, 1e-6, D.ptr(st.ll), D.ptr(st.sync),
-                               None, None, None, None, sp)
+                               None, None, None, None, None, 0, sp)
     L.dr_graph_end(sp, ctypes.byref(g))
     try:
         for rep in range(4):
@@ -255,7 +255,7 @@ def test_step_gives_up_loudly_when_a_previous_call_timed_out():
         st.sync[1] = 1
         xd = dev(x0)
         args = [D.ptr(st.table), 2, D.ptr(xd), 64, H, I, TOPK, 1e-6, D.ptr(st.ll), D.ptr(st.sync), None, None, None,
-                None, D.stream_ptr()]
+                None, None, 0, D.stream_ptr()]
         assert L.raw("dr_moe_decode_step_bf16s")(*args) == 0
         assert L.raw("dr_stream_sync")(D.stream_ptr()) == 9001
         assert np.isnan(host(xd)).all(), "a call that gave up must leave x all NaN"
@@ -300,7 +300,7 @@ def _busy_stream_step(limit_us):
         main = torch.cuda.current_stream()
         rc = L.raw("dr_moe_decode_step_bf16s")(D.ptr(st.table), 2, D.ptr(xd), 64, H, I, TOPK, 1e-6, D.ptr(st.ll),
                                                D.ptr(st.sync), D.ptr(idx), D.ptr(wts), D.ptr(sg), D.ptr(xs),
-                                               main.cuda_stream)
+                                               None, 0, main.cuda_stream)
         assert rc == 0
         code = L.raw("dr_stream_sync")(main.cuda_stream)
         side.synchronize()
@@ -340,3 +340,28 @@ def test_step_beside_a_busy_stream_is_correct_or_reports(record_property):
                       "DR_ERR_STEP_TIMEOUT (x poisoned with NaN)")
         assert code == 9001
         assert int(host(st.sync)[1]) == 1 and np.isnan(xf).any()
+
+
+def test_step_prefetch_range_changes_nothing():
+    """pf / pf_bytes (the next op's weights, warmed after the last layer) leave every result bit
+    unchanged, for ranges of odd sizes and one larger than the grid's share per thread."""
+    import torch
+
+    st = Stack([61, 62], 64, "cfg")
+    x0 = np.random.default_rng(21).normal(0, 1, H).astype(np.float32)
+    want = host(dev(x0))
+    xa = dev(x0)
+    st.run(xa)
+    want = host(xa)
+    for nbytes in (1, 1000, 4 << 20, (40 << 20) + 12345):
+        buf = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda")
+        st.sync.zero_()
+        st.ll.zero_()
+        xb = dev(x0)
+        torch.cuda.synchronize()
+        assert D.lib().raw("dr_moe_decode_step_bf16s")(D.ptr(st.table), 2, D.ptr(xb), 64, H, I, TOPK, 1e-6,
+                                                       D.ptr(st.ll), D.ptr(st.sync), None, None, None, None,
+                                                       D.ptr(buf), nbytes, D.stream_ptr()) == 0
+        torch.cuda.synchronize()
+        assert int(host(st.sync)[1]) == 0
+        np.testing.assert_array_equal(bits(host(xb)), bits(want), err_msg=f"pf_bytes {nbytes}")

@@ -21,7 +21,7 @@ def _run_noalloc(st, x_dev):
     sg = torch.zeros(n, device="cuda")
     xs = torch.zeros(n * H, device="cuda")
     D.lib().dr_moe_decode_step_bf16s_noalloc(D.ptr(st.table), n, D.ptr(x_dev), st.E, H, I, TOPK, 1e-6, D.ptr(idx),
-                                             D.ptr(wts), D.ptr(sg), D.ptr(xs), D.stream_ptr())
+                                             D.ptr(wts), D.ptr(sg), D.ptr(xs), None, 0, D.stream_ptr())
     torch.cuda.synchronize()
     return host(idx), host(wts), host(sg), host(xs)
 
@@ -46,7 +46,7 @@ def test_noalloc_step_rejects_bad_shapes():
     st = Stack([1], 16, "cfg")
     x = dev(np.zeros(H, np.float32))
     f = D.lib().raw("dr_moe_decode_step_bf16s_noalloc")
-    base = [D.ptr(st.table), 1, D.ptr(x), 16, H, I, TOPK, 1e-6, None, None, None, None, D.stream_ptr()]
+    base = [D.ptr(st.table), 1, D.ptr(x), 16, H, I, TOPK, 1e-6, None, None, None, None, None, 0, D.stream_ptr()]
     for pos, bad in ((1, 0), (1, 1366), (3, 257), (4, 1024), (5, 256), (6, 4)):
         a = list(base)
         a[pos] = bad
@@ -67,14 +67,14 @@ sp = torch.cuda.current_stream().cuda_stream
 # first call of the library in this process: the no-allocation entry point, then the same call
 # captured into a graph and replayed
 assert L.raw("dr_moe_decode_step_bf16s_noalloc")(D.ptr(st.table), 2, D.ptr(xa), 16, H, I, TOPK, 1e-6,
-                                                  None, None, None, None, sp) == 0
+                                                  None, None, None, None, None, 0, sp) == 0
 torch.cuda.synchronize()
 s2 = torch.cuda.Stream(); p2 = s2.cuda_stream
 xg = torch.from_numpy(x0).cuda(); torch.cuda.synchronize()
 g = ctypes.c_void_p()
 assert L.raw("dr_graph_begin")(p2) == 0
 assert L.raw("dr_moe_decode_step_bf16s_noalloc")(D.ptr(st.table), 2, D.ptr(xg), 16, H, I, TOPK, 1e-6,
-                                                  None, None, None, None, p2) == 0
+                                                  None, None, None, None, None, 0, p2) == 0
 assert L.raw("dr_graph_end")(p2, ctypes.byref(g)) == 0
 for rep in range(3):
     xg.copy_(torch.from_numpy(x0).cuda()); torch.cuda.synchronize()

@@ -190,6 +190,32 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
                   note="router GEMM + top-k with grouping + grouped GEMM (token rows read through the slot map) + combine" + (
                       ", the shared expert on a second stream beside them" if pf.overlap else " + shared, one stream")
                        + "; us_graph: replayed from a HIP graph")
+    # the same 300 rows' experts (routing of the last uniform call) two ways: the grouped MFMA
+    # path (grouping, gate_up, down, combine, shared expert) and the small-batch GEMV kernels
+    # (dr_moe_decode_rows_bf16s: each weight row read once per 60-row call and multiplied by
+    # every row routed to it with VALU FMAs), 5 calls of 60 rows
+    pf.grouped = False
+    ms_mfma = timed(lambda i: pf.experts(lib, layers[i % nl]), iters, st)
+    P = D.ptr
+    rows_c = 60
+    xg = pf.x.clone()
+    act_g = torch.zeros(rows_c * (TOPK + 1) * I, device="cuda")
+
+    def gemv_path(i):
+        L = layers[i % nl]
+        for r0 in range(0, pf.rows, rows_c):
+            xr = xg[r0:r0 + rows_c]
+            lib.dr_moe_decode_rows_bf16s(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(L["sgu_q"]),
+                                         P(L["sgu_s"]), P(L["sd_q"]), P(L["sd_s"]), P(xr), P(pf.idx[r0 * TOPK:]),
+                                         P(pf.wts[r0 * TOPK:]), P(pf.sg[r0:]), P(xr), P(act_g), P(xr), None, rows_c,
+                                         H, I, TOPK, None, 1e-6, pf.sp)
+
+    ms_gemv = timed(gemv_path, max(4, iters // 4), st)
+    mfma_vs_gemv = {"mfma_grouped_us": round(ms_mfma * 1000, 2), "gemv_rows_us": round(ms_gemv * 1000, 2),
+                    "rows_per_expert_mean": round(pf.n / max(1, hit), 2),
+                    "note": "experts of one 300-row layer (routing given): grouped MFMA kernels (grouping, gate_up, "
+                            "down, combine, shared expert) against the small-batch GEMV kernels "
+                            "(dr_moe_decode_rows_bf16s, 5 calls of 60 rows, shared expert and residual included)"}
     # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
     g = torch.Generator(device="cuda").manual_seed(31)
     hot = torch.randperm(E, generator=g, device="cuda")[: E // 10]
@@ -207,7 +233,8 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
     cnt2 = pf.counts.cpu()
     skew = rec(ms2 * 1000, nbytes2, experts_hit=hit2, rows_per_expert_max=int(cnt2.max()),
                note="skewed: 10% of experts get 50% of the pairs; routing given, no router GEMM")
-    return {"uniform": uniform, "skewed": skew, "shared_expert": shared_prefill_compare(lib, st, pf.rows)}
+    return {"uniform": uniform, "skewed": skew, "mfma_vs_gemv": mfma_vs_gemv,
+            "shared_expert": shared_prefill_compare(lib, st, pf.rows)}
 
 
 def shared_prefill_compare(lib, st, rows, iters=40, copies=8):

@@ -221,15 +221,19 @@ __global__ void __launch_bounds__(GR_THREADS)
     }
     if (lane == 0) sgate[r] = lg[sub][E];
   }
-  // hand-over to the last block: the block's idx stores happen before its count (workgroup
-  // barrier, then a release increment at agent scope); the block that sees the final count
-  // acquires it before any thread reads idx
+  // Hand-over to the last block.  The idx words are the only data handed over, and they are
+  // stored with agent-scope atomic stores (written through to the device-coherent level, not
+  // left in this XCD's L2); s_waitcnt(0) waits until those stores are acknowledged, the barrier
+  // orders every wave's acknowledgement before thread 0's count, and the last block reads idx
+  // with agent-scope atomic loads (not served from a possibly stale L2 line).  A release /
+  // acquire pair on the count would instead write back and invalidate the whole L2 of each
+  // block's XCD: measured 12.1 -> 14.4 us for this kernel at 300 rows.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   group_block([&](int i) { return __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
               rows * topk, E, counts, offsets, slot_of, 0, nullptr, row_of_slot, topk);
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

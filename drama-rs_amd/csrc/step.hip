@@ -51,7 +51,7 @@ constexpr int ST_MAXL = (ST_TAG_STRIDE - 1) / 3;
 // policies below) were measured on MI355X
 // (configuration 3: 13.9 us/layer with per-wave delays counted from each wave's own arrival,
 // 11.9 us/layer with these; 10 ticks earlier than the activation offset already costs 0.3 us).
-constexpr uint32_t ST_DLY_ROUND = 20;  // between poll rounds; the first-poll offsets are per format
+constexpr uint32_t ST_DLY_ROUND = 15;  // between poll rounds (15: 9.93, 20: 9.95, 30: 10.5 us/layer); the first-poll offsets are per format
 constexpr uint64_t ST_DEFER_SIBLING = 55;  // ticks after the layer start at which waves 4 and 5 begin the norm
 constexpr uint64_t ST_TIMEOUT_TICKS = 20000000;  // default wait limit; s_memrealtime runs at 100 MHz: 0.2 s
 
@@ -244,12 +244,15 @@ struct StepQ4 {
   // 140-160 -> 11.15-11.2 us/layer)
   // (kOffX, with the in-band activation phase and kOffActIb 375-385: 175 -> 11.0, 185-195 -> 10.85-10.95,
   // 215 -> 11.1 us/layer)
-  static constexpr uint32_t kOffL = 145, kOffAct = 355, kOffX = 190;
+  // (retuned after the start-up and exchange changes, as a grid over kOffX x kOffActIb: kOffX 150 ->
+  // 10.44, 160-175 -> 10.02-10.07, 190 -> 10.23, 205 -> 10.39 us/layer; with kOffActIb 330: kOffX 165
+  // -> 9.93-9.95; kOffActIb 310 -> 10.43, 320 -> 10.14, 330-340 -> 9.94-9.96, 360 -> 10.20)
+  static constexpr uint32_t kOffL = 145, kOffAct = 355, kOffX = 165;
   static constexpr uint32_t kOffXA32 = 235;  // residual offset with the full-fp32 activation exchange
                                              // (190 -> 11.95, 215 -> 11.6-11.7, 235 -> 11.5 us/layer)
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
   // 400 -> 11.5 us/layer)
-  static constexpr uint32_t kOffActIb = 345;  // (335-350 with the early gate_up loads: 10.7 us/layer)
+  static constexpr uint32_t kOffActIb = 330;  // (335-350 with the early gate_up loads: 10.7 us/layer)
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -337,10 +340,13 @@ struct StepFP8 {
   // first-poll offsets (measured; kOffAct: twice the gate_up bytes of int4; kOffX: 165-175 ->
   // 11.4-11.6, 205 -> 12.0, 245 -> 12.3 us/layer)
   // (kOffL: 135-160 -> 11.36-11.41, 185 -> 11.66 us/layer)
-  static constexpr uint32_t kOffL = 150, kOffAct = 430, kOffX = 155;  // (kOffX 140-165: 11.2-11.3 us/layer)
+  // (retuned with the int4 policy's changes: kOffActIb 445 -> 10.83, 485 -> 11.23 us/layer against 11.04
+  // at 465; kOffL 135 -> 10.87, 165 -> 11.18; kOffX 140 -> 10.89, 170 -> 11.16; together kOffL 135,
+  // kOffX 140, kOffActIb 430: 10.55-10.7; kOffX 125 -> 10.96, kOffL 120 with kOffX 125 -> 11.28)
+  static constexpr uint32_t kOffL = 135, kOffAct = 430, kOffX = 140;
   static constexpr uint32_t kOffXA32 = 165;
   // in-band activation phase: 400 -> 12.6, 430 -> 11.8, 460-470 -> 11.7, 510 -> 12.0 us/layer
-  static constexpr uint32_t kOffActIb = 465;
+  static constexpr uint32_t kOffActIb = 430;
   DEV static int xslot(int f) { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
   struct GU {
     uint4 g[2][2], u[2][2];

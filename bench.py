@@ -248,7 +248,7 @@ def main():
         for L in layers:
             record_layer(L)
 
-    def config2_single_layer(iters=200):
+    def config2_single_layer(iters=200, extras=True):
         # one decode layer per call (the fused step over one layer, and the per-layer chain),
         # rotating over the resident layers so that no call finds its weights in the MALL
         import benchcfg
@@ -264,15 +264,18 @@ def main():
             assert rc == 0
 
         out = {}
-        for key, fn in (("fused_one_layer", fused_one), ("fused_one_layer_warm_next", fused_one_warm),
-                        ("chain_one_layer", lambda i: record_layer(layers[i % nl]))):
+        runs = [("fused_one_layer", fused_one), ("chain_one_layer", lambda i: record_layer(layers[i % nl]))]
+        if extras:
+            runs.insert(1, ("fused_one_layer_warm_next", fused_one_warm))
+        for key, fn in runs:
             ms = benchcfg.timed(fn, iters, st)
             out[key] = benchcfg.rec(ms * 1000, bytes_step // nl)
             out[key]["us_graph"] = round(benchcfg.timed_graph(fn, iters, st, nl) * 1000, 2)
         out["note"] = ("one launch (fused) or three launches (chain) per layer, launch latency included; "
                        "_warm_next: each step launch warms the next layer's dense block (router, norm weight, "
                        "shared expert: pf/pf_bytes) during its last layer")
-        out["engine_sequence"] = engine_sequence(iters)
+        if extras:
+            out["engine_sequence"] = engine_sequence(iters)
         return out
 
     def engine_sequence(iters):
@@ -325,7 +328,9 @@ def main():
     if args.profile_small:
         import benchcfg
 
-        print(json.dumps({"cfg2_one_layer": config2_single_layer(), "cfg1_gemv_int4": benchcfg.config1_gemv(lib, st)}))
+        # (without the warm and engine-order variants, so that each kernel in the trace is one path)
+        print(json.dumps({"cfg2_one_layer": config2_single_layer(extras=False),
+                          "cfg1_gemv_int4": benchcfg.config1_gemv(lib, st)}))
         return
 
     # ---- parity spot check: layer 0 of the first step against the CPU oracle

@@ -216,8 +216,8 @@ __global__ void __launch_bounds__(512)
 // 2) and row_ror (o = 4: by 12 for the lanes whose partner is l + 4, by 4 for l - 4; o = 8: by
 // 8), v_permlane16_swap / v_permlane32_swap (o = 16, 32; the swap itself hands each lane the
 // half it keeps).  A and W chunks of the next j are requested before the current j's FMAs.
-// Measured at 300 x 257 x 2048: 12.0 us (a 2 x 8 per-wave kernel with one butterfly per dot: 16.8 us); 4 x 8 tiles (twice the waves,
-// more conversions per FMA) 13.9 us.
+// Measured at 300 x 257 x 2048 with 8 x 8 tiles: 12.0 us (a 2 x 8 per-wave kernel with one butterfly
+// per dot: 16.8 us); 4 x 8 tiles (twice the waves, more conversions per FMA) 13.9 us.
 template <int O, int V>
 DEV void rs_step(float (&v)[64]) {
   const int lane = lane_id();
@@ -238,15 +238,21 @@ DEV void rs_step(float (&v)[64]) {
   }
 }
 
-template <int NCH>
+// Tiles of TM x TN outputs (at most 8 x 8: the 64 reduce-scatter slots; the unused slots stay
+// zero and are never stored).  8 x 5 balances 300 x 257 best over the 1024 SIMDs: measured 9.5-9.8
+// us against 10.7-11.2 for 8 x 8 (1254 tiles, a fifth of the SIMDs running two), 9.8 for 8 x 6,
+// 10.1-10.3 for 8 x 7 and 12.1 for 8 x 4 (more A loads per FMA), with identical bits.
+constexpr int GT_TM = 8, GT_TN = 5;
+template <int NCH, int TM = GT_TM, int TN = GT_TN>
 __global__ void __launch_bounds__(256)
     k_gemm_tile(const uint16_t* __restrict__ A, const uint16_t* __restrict__ W, float* __restrict__ C, int M, int N,
                 int K, float beta) {
 #pragma clang fp contract(off)
+  static_assert(TM >= 1 && TM <= 8 && TN >= 1 && TN <= 8, "tile of at most 8 x 8 (64 reduce-scatter slots)");
   const int lane = lane_id();
-  const int tn = (N + 7) >> 3;
+  const int tn = (N + TN - 1) / TN;
   const int tile = blockIdx.x * 4 + wave_id();
-  const int m0 = (tile / tn) * 8, n0 = (tile % tn) * 8;
+  const int m0 = (tile / tn) * TM, n0 = (tile % tn) * TN;
   if (m0 >= M) return;
   const int KC = K / 8;
   const uint16_t* ap[8];
@@ -256,6 +262,7 @@ __global__ void __launch_bounds__(256)
     ap[r] = A + (size_t)(m0 + r < M ? m0 + r : M - 1) * K + (size_t)lane * 8;
     wp[r] = W + (size_t)(n0 + r < N ? n0 + r : N - 1) * K + (size_t)lane * 8;
   }
+  (void)ap, (void)wp;
   float acc[64];
 #pragma unroll
   for (int i = 0; i < 64; ++i) acc[i] = 0.f;
@@ -264,8 +271,8 @@ __global__ void __launch_bounds__(256)
     const bool in = lane + WAVE * j < KC;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      ac[b][r] = in ? ld16(ap[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
-      wc[b][r] = in ? ld16(wp[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
+      if (r < TM) ac[b][r] = in ? ld16(ap[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
+      if (r < TN) wc[b][r] = in ? ld16(wp[r] + (size_t)j * WAVE * 8) : make_uint4(0, 0, 0, 0);
     }
   };
   load(0, 0);
@@ -279,15 +286,19 @@ __global__ void __launch_bounds__(256)
         float a[8], w[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          const uint32_t aw = e < 2 ? ac[b][r].x : e < 4 ? ac[b][r].y : e < 6 ? ac[b][r].z : ac[b][r].w;
-          const uint32_t ww = e < 2 ? wc[b][r].x : e < 4 ? wc[b][r].y : e < 6 ? wc[b][r].z : wc[b][r].w;
-          a[r] = (e & 1) ? bf16_hi(aw) : bf16_lo(aw);
-          w[r] = (e & 1) ? bf16_hi(ww) : bf16_lo(ww);
+          if (r < TM) {
+            const uint32_t aw = e < 2 ? ac[b][r].x : e < 4 ? ac[b][r].y : e < 6 ? ac[b][r].z : ac[b][r].w;
+            a[r] = (e & 1) ? bf16_hi(aw) : bf16_lo(aw);
+          }
+          if (r < TN) {
+            const uint32_t ww = e < 2 ? wc[b][r].x : e < 4 ? wc[b][r].y : e < 6 ? wc[b][r].z : wc[b][r].w;
+            w[r] = (e & 1) ? bf16_hi(ww) : bf16_lo(ww);
+          }
         }
 #pragma unroll
-        for (int m = 0; m < 8; ++m)
+        for (int m = 0; m < TM; ++m)
 #pragma unroll
-          for (int n = 0; n < 8; ++n) acc[8 * m + n] = __builtin_fmaf(w[n], a[m], acc[8 * m + n]);
+          for (int n = 0; n < TN; ++n) acc[8 * m + n] = __builtin_fmaf(w[n], a[m], acc[8 * m + n]);
       }
     }
   }
@@ -299,7 +310,7 @@ __global__ void __launch_bounds__(256)
   rs_step<32, 2>(acc);
   const int i = (int)(__builtin_bitreverse32((uint32_t)lane) >> 26);
   const int m = m0 + (i >> 3), n = n0 + (i & 7);
-  if (m < M && n < N) {
+  if ((i >> 3) < TM && (i & 7) < TN && m < M && n < N) {
     float* c = C + (size_t)m * N + n;
     *c = beta == 0.f ? acc[0] : acc[0] + beta * *c;
   }
@@ -311,7 +322,7 @@ void launch_gemm(const uint16_t* A, const uint16_t* W, float* C, int M, int N, i
     hipLaunchKernelGGL(k_gemm_rows<NCH>, dim3((N + 7) / 8), dim3(512), 0, st, A, W, C, M, N, K, beta);
     return;
   }
-  const int tiles = ((M + 7) / 8) * ((N + 7) / 8);
+  const int tiles = ((M + GT_TM - 1) / GT_TM) * ((N + GT_TN - 1) / GT_TN);
   hipLaunchKernelGGL(k_gemm_tile<NCH>, dim3((tiles + 3) / 4), dim3(256), 0, st, A, W, C, M, N, K, beta);
 }
 

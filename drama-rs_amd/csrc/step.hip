@@ -247,12 +247,16 @@ struct StepQ4 {
   // (retuned after the start-up and exchange changes, as a grid over kOffX x kOffActIb: kOffX 150 ->
   // 10.44, 160-175 -> 10.02-10.07, 190 -> 10.23, 205 -> 10.39 us/layer; with kOffActIb 330: kOffX 165
   // -> 9.93-9.95; kOffActIb 310 -> 10.43, 320 -> 10.14, 330-340 -> 9.94-9.96, 360 -> 10.20)
-  static constexpr uint32_t kOffL = 145, kOffAct = 355, kOffX = 165;
+  // (retuned for the integer-digit gate_up dots, whose pairs are done ~0.4 us sooner: kOffActIb 330 ->
+  // 10.11, 310 -> 9.88, 290-300 -> 9.85 with kOffX 165, 9.68-9.70 with kOffX 180 (170 -> 9.75, 195 -> 9.84,
+  // 210 -> 9.96); kOffL 125 -> 9.64, 130 -> 9.57, 135 -> 9.59, 140 -> 9.64, 155 -> 9.78 us/layer)
+  static constexpr uint32_t kOffL = 130, kOffAct = 300, kOffX = 180;
   static constexpr uint32_t kOffXA32 = 235;  // residual offset with the full-fp32 activation exchange
                                              // (190 -> 11.95, 215 -> 11.6-11.7, 235 -> 11.5 us/layer)
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,
-  // 400 -> 11.5 us/layer)
-  static constexpr uint32_t kOffActIb = 330;  // (335-350 with the early gate_up loads: 10.7 us/layer)
+  // 400 -> 11.5 us/layer); full-fp32 activations with the integer-digit dots: kOffAct 355 -> 11.06,
+  // 340 -> 10.85, 320 -> 10.73, 300 -> 10.55-10.61, 285 -> 10.70, 270 -> 11.10 us/layer
+  static constexpr uint32_t kOffActIb = 295;  // (335-350 with the early gate_up loads: 10.7 us/layer)
   DEV static int xslot(int f) { return slot_q4(f); }
   struct GU {
     uint4 wg[2], wu[2];
@@ -271,24 +275,39 @@ struct StepQ4 {
       g.su[p] = ld4(sm + (size_t)(I + j) * (H / 64));
     }
   }
+  // x of lane l's chunk (inputs 32 l .. 32 l + 31) as 24-bit fixed point X = x 2^S (S per chunk,
+  // |X| <= 2^22) in six balanced base-16 digits, each digit of 8 inputs packed as the int4
+  // nibbles of one word (stage_xq); the weights' nibbles q become q - 8 (xor 8), so
+  // sum (q - 8) X is six exact v_dot8 sums per word, and w x = s (q - 8) x + (m + 8 s) x
   DEV static void gate_up(const GU& g, const float4* xq4, const float* s_xsum, int lane, float (&av)[2]) {
-    float xv[32];
-    const float xsum = s_xsum[lane];
+    const uint4* xd4 = reinterpret_cast<const uint4*>(xq4);
+    uint32_t dg[24];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = xq4[i * 64 + lane];
-      xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
+    for (int j = 0; j < 6; ++j) {
+      const uint4 v = xd4[j * 64 + lane];
+      dg[4 * j] = v.x, dg[4 * j + 1] = v.y, dg[4 * j + 2] = v.z, dg[4 * j + 3] = v.w;
     }
+    const float xsum = s_xsum[lane], xsc = s_xsum[64 + lane];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      float qg = 0.f, qu = 0.f;
-      qg = dot8_q4(g.wg[p].x, xv + 0, qg), qu = dot8_q4(g.wu[p].x, xv + 0, qu);
-      qg = dot8_q4(g.wg[p].y, xv + 8, qg), qu = dot8_q4(g.wu[p].y, xv + 8, qu);
-      qg = dot8_q4(g.wg[p].z, xv + 16, qg), qu = dot8_q4(g.wu[p].z, xv + 16, qu);
-      qg = dot8_q4(g.wg[p].w, xv + 24, qg), qu = dot8_q4(g.wu[p].w, xv + 24, qu);
+      int ag[6] = {0, 0, 0, 0, 0, 0}, au[6] = {0, 0, 0, 0, 0, 0};
+      const uint32_t wg[4] = {g.wg[p].x, g.wg[p].y, g.wg[p].z, g.wg[p].w};
+      const uint32_t wu[4] = {g.wu[p].x, g.wu[p].y, g.wu[p].z, g.wu[p].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int qg = (int)(wg[w] ^ 0x88888888u), qu = (int)(wu[w] ^ 0x88888888u);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          ag[k] = __builtin_amdgcn_sdot8(qg, (int)dg[6 * w + k], ag[k], false);
+          au[k] = __builtin_amdgcn_sdot8(qu, (int)dg[6 * w + k], au[k], false);
+        }
+      }
+      float dgv = (float)ag[5], duv = (float)au[5];
+#pragma unroll
+      for (int k = 4; k >= 0; --k) dgv = __builtin_fmaf(dgv, 16.f, (float)ag[k]), duv = __builtin_fmaf(duv, 16.f, (float)au[k]);
       const float2 a = SC::pair(g.sg[p]), b = SC::pair(g.su[p]);
-      const float gv = wave_sum(a.x * qg + a.y * xsum);
-      const float uv = wave_sum(b.x * qu + b.y * xsum);
+      const float gv = wave_sum(a.x * (dgv * xsc) + __builtin_fmaf(8.f, a.x, a.y) * xsum);
+      const float uv = wave_sum(b.x * (duv * xsc) + __builtin_fmaf(8.f, b.x, b.y) * xsum);
       av[p] = silu(gv) * uv;
     }
   }
@@ -452,7 +471,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   __shared__ float lg[ST_MAXE + 1];
   __shared__ int s_sel[ST_WPB][ST_TOPK];  // every wave's copy of the picks
   __shared__ float s_asum[192];  // activation chunk sums (see SpecAct::post)
-  __shared__ float s_xsum[64];   // int4: sums of the 32-input chunks of xn (lane l's chunk)
+  __shared__ float s_xsum[128];  // int4: sums of the 32-input chunks of xn (lane l's chunk), then their 2^-S
   __shared__ uint64_t s_cand[32];  // per-group top 8 (canon_cand64)
   __shared__ int s_abort;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -530,15 +549,37 @@ __global__ void __launch_bounds__(ST_NT, 1)
 #pragma unroll
       for (int j = 0; j < 8; ++j) xr[j] = xr4[lane + 64 * j];
       const float inv = Ly.nw ? canon_rms_inv_regs<8>(xr, eps) : 1.f;
-      // this thread's slot of the normalised x (and the int4 chunk sums), needed from gate_up on;
-      // the router waves do it after their router row
+      // this thread's part of the normalised x as gate_up reads it (int4: the chunk sums, scales
+      // and fixed-point digits; FP8: the floats in their lane slots); the router waves do it after
+      // their router row
       auto stage_xq = [&]() {
         const float4 xn = canon_norm4(xr4[tid], inv, nwv);
-        xq4[F::xslot(tid)] = xn;
+        if constexpr (!F::kMinTerm) xq4[F::xslot(tid)] = xn;
         if constexpr (F::kMinTerm) {
           float t = (xn.x + xn.y) + (xn.z + xn.w);  // threads 8c..8c+7 hold chunk c
           t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
-          if ((lane & 7) == 0) s_xsum[tid >> 3] = t;
+          float mx = fmaxf(fmaxf(fabsf(xn.x), fabsf(xn.y)), fmaxf(fabsf(xn.z), fabsf(xn.w)));
+          mx = xmax_step<1>(mx), mx = xmax_step<2>(mx), mx = xmax_step<4>(mx);
+          // chunk max below 2^e; X = x 2^(22 - e), |X| <= 2^22
+          const int e = (int)((__float_as_uint(mx) >> 23) & 0xff) - 126;
+          const int sh = 22 - e;
+          if ((lane & 7) == 0) s_xsum[tid >> 3] = t, s_xsum[64 + (tid >> 3)] = __builtin_ldexpf(1.f, -sh);
+          // V = (X + 0x888888) ^ 0x888888: nibble k of V is balanced digit k of X as an int4
+          const float xv4[4] = {xn.x, xn.y, xn.z, xn.w};
+          uint32_t V[4];
+#pragma unroll
+          for (int t4 = 0; t4 < 4; ++t4) V[t4] = ((uint32_t)__float2int_rn(__builtin_ldexpf(xv4[t4], sh)) + 0x888888u) ^ 0x888888u;
+          // digit word (chunk c, 8-group gi, digit k) at 32-bit word ((gi 6 + k) / 4 * 64 + c) * 4 + (gi 6 + k) % 4;
+          // this thread holds inputs 4 h .. 4 h + 3 of the group: half h of the word
+          uint16_t* xd = reinterpret_cast<uint16_t*>(xq4);
+          const int c = tid >> 3, gi = (tid & 7) >> 1, h = tid & 1;
+#pragma unroll
+          for (int k = 0; k < 6; ++k) {
+            const uint32_t hw = ((V[0] >> (4 * k)) & 15u) | (((V[1] >> (4 * k)) & 15u) << 4) |
+                                (((V[2] >> (4 * k)) & 15u) << 8) | (((V[3] >> (4 * k)) & 15u) << 12);
+            const int j = gi * 6 + k;
+            xd[(((j >> 2) * 64 + c) * 4 + (j & 3)) * 2 + h] = (uint16_t)hw;
+          }
         }
       };
       if (!is_router) stage_xq();

@@ -3,6 +3,7 @@
 // Everything here is written for CDNA4 wave64: a "wave" is 64 lanes, reductions are xor
 // butterflies over 64 lanes.  Half-precision values travel as raw 16-bit patterns.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -235,6 +236,66 @@ DEV float dot8_q4(uint32_t w, const float* x, float acc) {
   return acc;
 }
 
+// ---- int4 dots against fixed-point digits of x ---------------------------------------------
+// A 32-input chunk c of x (the chunk lane c of an int4 row dot owns) is written as 24-bit fixed
+// point X = x 2^S, S per chunk from its largest exponent e (every |x| < 2^e, S = 22 - e, so
+// |X| <= 2^22), in six balanced base-16 digits: V = (X + 0x888888) ^ 0x888888 has digit k of X
+// as the int4 nibble k.  Digit k of the 8 inputs of group g of the chunk is one word (nibble i =
+// input 8 g + i, as the weight words), at word ((j >> 2) * 64 + c) * 4 + (j & 3), j = 6 g + k,
+// so lane c reads its 24 words as six 16-byte LDS reads with no bank conflicts.  A weight word
+// xor 0x88888888 holds q - 8 as int4 nibbles, and sum (q - 8) X is six exact v_dot8 sums;
+// q4_dot_digits returns it as a float (one rounding) and the caller forms
+// w . x = s 2^-S sum (q - 8) X + (m + 8 s) sum x.
+// Staging: the 8 threads of a chunk (consecutive lanes, part = lane & 7, thread part holding
+// inputs 4 part .. 4 part + 3 as xn) each call q4_digits_stage; it also leaves the chunk's sum
+// in csum[c] and 2^-S in cscale[c].
+DEV void q4_digits_stage(float4 xn, int c, int part, uint32_t* xd, float* csum, float* cscale) {
+  float t = (xn.x + xn.y) + (xn.z + xn.w);
+  t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
+  float mx = fmaxf(fmaxf(fabsf(xn.x), fabsf(xn.y)), fmaxf(fabsf(xn.z), fabsf(xn.w)));
+  mx = xmax_step<1>(mx), mx = xmax_step<2>(mx), mx = xmax_step<4>(mx);
+  const int e = (int)((__float_as_uint(mx) >> 23) & 0xff) - 126;
+  const int sh = 22 - e;
+  if (part == 0) csum[c] = t, cscale[c] = __builtin_ldexpf(1.f, -sh);
+  const float xv4[4] = {xn.x, xn.y, xn.z, xn.w};
+  uint32_t V[4];
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4) V[t4] = ((uint32_t)__float2int_rn(__builtin_ldexpf(xv4[t4], sh)) + 0x888888u) ^ 0x888888u;
+  // this thread holds inputs 4 h .. 4 h + 3 of group gi: half h of each digit word
+  uint16_t* xh = reinterpret_cast<uint16_t*>(xd);
+  const int gi = part >> 1, h = part & 1;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const uint32_t hw = ((V[0] >> (4 * k)) & 15u) | (((V[1] >> (4 * k)) & 15u) << 4) |
+                        (((V[2] >> (4 * k)) & 15u) << 8) | (((V[3] >> (4 * k)) & 15u) << 12);
+    const int j = gi * 6 + k;
+    xh[(((j >> 2) * 64 + c) * 4 + (j & 3)) * 2 + h] = (uint16_t)hw;
+  }
+}
+DEV void q4_digits_load(const uint32_t* xd, int lane, uint32_t (&dg)[24]) {
+  const uint4* xd4 = reinterpret_cast<const uint4*>(xd);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const uint4 v = xd4[j * 64 + lane];
+    dg[4 * j] = v.x, dg[4 * j + 1] = v.y, dg[4 * j + 2] = v.z, dg[4 * j + 3] = v.w;
+  }
+}
+// sum over the lane's 32 inputs of (q - 8) X for the weight words w (inputs 8 g .. 8 g + 7 in w[g])
+DEV float q4_dot_digits(const uint4& w, const uint32_t (&dg)[24]) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  int a[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int q = (int)(ww[g] ^ 0x88888888u);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) a[k] = __builtin_amdgcn_sdot8(q, (int)dg[6 * g + k], a[k], false);
+  }
+  float d = (float)a[5];
+#pragma unroll
+  for (int k = 4; k >= 0; --k) d = __builtin_fmaf(d, 16.f, (float)a[k]);
+  return d;
+}
+
 // Sum of 4 int8 values of w times x[0..3], computed as sum((b ^ 0x80) x) - 128 sum(x): the
 // caller subtracts 128 * sum(x) once per row slice.
 DEV float dot4_u8b(uint32_t w, const float* x, float acc) {
@@ -262,19 +323,18 @@ DEV void warm_range(const char* pf, size_t bytes) {
   asm volatile("" ::"v"(acc));
 }
 
-// LDS slots of staged inputs, float4 f -> slot.  SlotQ4: lane l of a wave reads the 32 inputs
-// [32 l, 32 l + 32) of each 2048-input part as 8 float4 (slot i * 64 + l); SlotQ8H: lane l
-// reads the 16 inputs [16 l, 16 l + 16) of each 1024-input half as 4 float4.
-struct SlotQ4 {
-  DEV int operator()(int f) const { return (f & ~511) + (f & 7) * 64 + ((f & 511) >> 3); }
-};
+// LDS layouts of staged inputs.  SlotQ8H (float4 f -> slot): lane l reads the 16 inputs
+// [16 l, 16 l + 16) of each 1024-input half as 4 float4.  SlotQ4D: the row as the int4 dots'
+// fixed-point digits (q4_digits_stage; H = 2048): lane l's 32-input chunk as 24 digit words in
+// the first 6 KB of the row's 8 KB, then the 64 chunk sums and the 64 scales 2^-S.
+struct SlotQ4D {};
 struct SlotQ8H {
   DEV int operator()(int f) const { return (f & ~255) + (f & 3) * 64 + ((f & 255) >> 2); }
 };
 
 // Stage NR rows of RMSNorm(x) (nw == nullptr: x itself) in LDS, float4 f of a row at
-// Slot{}(f) (SlotQ4: the 32-element lane chunks of int4 rows; SlotQ8H: the 16-element lane
-// chunks of byte rows read as two 1024-byte halves).  load() issues the global loads unconditionally and ahead of everything issued after
+// Slot{}(f) (SlotQ8H: the 16-element lane chunks of byte rows read as two 1024-byte halves), or
+// as the digits of SlotQ4D.  load() issues the global loads unconditionally and ahead of everything issued after
 // it (loads return in order, so weight loads issued later do not delay the staging);
 // finish() reduces (partial sums added in wave order), normalises and writes LDS.  Every
 // thread of the block calls both.
@@ -324,7 +384,12 @@ struct XStage {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int f = threadIdx.x + NT * i;
-        xs[r * (H / 4) + Slot{}(f)] = v[r][i];
+        if constexpr (std::is_same<Slot, SlotQ4D>::value) {
+          float* rb = reinterpret_cast<float*>(xs + r * (H / 4));
+          q4_digits_stage(v[r][i], f >> 3, f & 7, reinterpret_cast<uint32_t*>(rb), rb + 1536, rb + 1600);
+        } else {
+          xs[r * (H / 4) + Slot{}(f)] = v[r][i];
+        }
       }
     __syncthreads();
   }

@@ -2,11 +2,11 @@
 // src/ffi.rs:42-46) and the single int4 GEMV of benchmark configuration 1.
 //
 // gfx950 mapping.  A K = 2048 int4 row is 1024 bytes: exactly one 16-byte load per lane of a
-// wave64, so lane l always owns elements [32 l, 32 l + 32) and half of group l / 2.  Its 32
-// normalised inputs therefore live in registers for every row the wave touches; they are
-// staged once per block through LDS in a lane-major swizzle (slot = i * 64 + lane) so the
-// 16-byte LDS reads are conflict free.  Each lane folds scale and min into its partial dot:
-// s * sum(q x) + m * sum(x), and one 64-lane butterfly finishes the row.
+// wave64, so lane l always owns elements [32 l, 32 l + 32) and half of group l / 2.  gate_up
+// stages its 32 normalised inputs once per block in LDS as 24-bit fixed-point digits
+// (q4_digits_stage, read back with conflict-free 16-byte reads), so each weight word is six
+// exact v_dot8 sums; each lane folds scale and min into its partial dot,
+// s 2^-S sum((q - 8) X) + (m + 8 s) sum(x), and one 64-lane butterfly finishes the row.
 //
 // Down projection: one output row n gathers 8 expert rows of 256 bytes plus the 512-byte
 // int8 shared row.  Lane l owns chunk (l & 15) of experts (l >> 4) and 4 + (l >> 4) and 8
@@ -41,7 +41,7 @@ __global__ void __launch_bounds__(WPB * 64)
   const int lane = lane_id(), wave = wave_id();
   if ((int)blockIdx.x >= NBS) {
     const int g = (blockIdx.x - NBS) * WPB + wave;
-    XStage<H, NT, B, SlotQ4> xst;
+    XStage<H, NT, B, SlotQ4D> xst;
     xst.load(x, nw);
     uint4 wg[D], wu[D];
     uint32_t sg[D], su[D];
@@ -61,23 +61,17 @@ __global__ void __launch_bounds__(WPB * 64)
     for (int p = 0; p < PPW; ++p) {
       const int d = p % D;
       const int u = g + NW * p, b = u / (DEC_TOPK * I), k = (u / I) % DEC_TOPK, j = u % I;
-      float xv[32], xsum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float4 v = xs[b * (H / 4) + i * 64 + lane];
-        xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
-        xsum += (v.x + v.y) + (v.z + v.w);
-      }
+      // row b of x as fixed-point digits (XStage with SlotQ4D): w . x = s (q - 8) . x + (m + 8 s) sum x
+      const float* rb = reinterpret_cast<const float*>(xs + b * (H / 4));
+      uint32_t dg[24];
+      q4_digits_load(reinterpret_cast<const uint32_t*>(rb), lane, dg);
+      const float xsum = rb[1536 + lane], xsc = rb[1600 + lane];
       opaque(wg[d]), opaque(wu[d]);
-      float qg = 0.f, qu = 0.f;
-      qg = dot8_q4(wg[d].x, xv + 0, qg), qu = dot8_q4(wu[d].x, xv + 0, qu);
-      qg = dot8_q4(wg[d].y, xv + 8, qg), qu = dot8_q4(wu[d].y, xv + 8, qu);
-      qg = dot8_q4(wg[d].z, xv + 16, qg), qu = dot8_q4(wu[d].z, xv + 16, qu);
-      qg = dot8_q4(wg[d].w, xv + 24, qg), qu = dot8_q4(wu[d].w, xv + 24, qu);
+      const float qg = q4_dot_digits(wg[d], dg), qu = q4_dot_digits(wu[d], dg);
       const float2 pa = SC::pair(sg[d]), pb = SC::pair(su[d]);
       if (p + D < PPW) issue(p + D, d);
-      const float gv = wave_sum(pa.x * qg + pa.y * xsum);
-      const float uv = wave_sum(pb.x * qu + pb.y * xsum);
+      const float gv = wave_sum(pa.x * (qg * xsc) + __builtin_fmaf(8.f, pa.x, pa.y) * xsum);
+      const float uv = wave_sum(pb.x * (qu * xsc) + __builtin_fmaf(8.f, pb.x, pb.y) * xsum);
       if (lane == 0) act[(size_t)b * (DEC_TOPK + 1) * I + k * I + j] = silu(gv) * uv;
     }
   } else {

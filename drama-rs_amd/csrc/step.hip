@@ -275,36 +275,15 @@ struct StepQ4 {
       g.su[p] = ld4(sm + (size_t)(I + j) * (H / 64));
     }
   }
-  // x of lane l's chunk (inputs 32 l .. 32 l + 31) as 24-bit fixed point X = x 2^S (S per chunk,
-  // |X| <= 2^22) in six balanced base-16 digits, each digit of 8 inputs packed as the int4
-  // nibbles of one word (stage_xq); the weights' nibbles q become q - 8 (xor 8), so
-  // sum (q - 8) X is six exact v_dot8 sums per word, and w x = s (q - 8) x + (m + 8 s) x
+  // x of lane l's chunk as the fixed-point digits of q4_digits_stage (stage_xq): each weight
+  // word is six exact v_dot8 sums, w x = s (q - 8) x + (m + 8 s) x
   DEV static void gate_up(const GU& g, const float4* xq4, const float* s_xsum, int lane, float (&av)[2]) {
-    const uint4* xd4 = reinterpret_cast<const uint4*>(xq4);
     uint32_t dg[24];
-#pragma unroll
-    for (int j = 0; j < 6; ++j) {
-      const uint4 v = xd4[j * 64 + lane];
-      dg[4 * j] = v.x, dg[4 * j + 1] = v.y, dg[4 * j + 2] = v.z, dg[4 * j + 3] = v.w;
-    }
+    q4_digits_load(reinterpret_cast<const uint32_t*>(xq4), lane, dg);
     const float xsum = s_xsum[lane], xsc = s_xsum[64 + lane];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      int ag[6] = {0, 0, 0, 0, 0, 0}, au[6] = {0, 0, 0, 0, 0, 0};
-      const uint32_t wg[4] = {g.wg[p].x, g.wg[p].y, g.wg[p].z, g.wg[p].w};
-      const uint32_t wu[4] = {g.wu[p].x, g.wu[p].y, g.wu[p].z, g.wu[p].w};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int qg = (int)(wg[w] ^ 0x88888888u), qu = (int)(wu[w] ^ 0x88888888u);
-#pragma unroll
-        for (int k = 0; k < 6; ++k) {
-          ag[k] = __builtin_amdgcn_sdot8(qg, (int)dg[6 * w + k], ag[k], false);
-          au[k] = __builtin_amdgcn_sdot8(qu, (int)dg[6 * w + k], au[k], false);
-        }
-      }
-      float dgv = (float)ag[5], duv = (float)au[5];
-#pragma unroll
-      for (int k = 4; k >= 0; --k) dgv = __builtin_fmaf(dgv, 16.f, (float)ag[k]), duv = __builtin_fmaf(duv, 16.f, (float)au[k]);
+      const float dgv = q4_dot_digits(g.wg[p], dg), duv = q4_dot_digits(g.wu[p], dg);
       const float2 a = SC::pair(g.sg[p]), b = SC::pair(g.su[p]);
       const float gv = wave_sum(a.x * (dgv * xsc) + __builtin_fmaf(8.f, a.x, a.y) * xsum);
       const float uv = wave_sum(b.x * (duv * xsc) + __builtin_fmaf(8.f, b.x, b.y) * xsum);
@@ -555,32 +534,8 @@ __global__ void __launch_bounds__(ST_NT, 1)
       auto stage_xq = [&]() {
         const float4 xn = canon_norm4(xr4[tid], inv, nwv);
         if constexpr (!F::kMinTerm) xq4[F::xslot(tid)] = xn;
-        if constexpr (F::kMinTerm) {
-          float t = (xn.x + xn.y) + (xn.z + xn.w);  // threads 8c..8c+7 hold chunk c
-          t = xsum_step<1>(t), t = xsum_step<2>(t), t = xsum_step<4>(t);
-          float mx = fmaxf(fmaxf(fabsf(xn.x), fabsf(xn.y)), fmaxf(fabsf(xn.z), fabsf(xn.w)));
-          mx = xmax_step<1>(mx), mx = xmax_step<2>(mx), mx = xmax_step<4>(mx);
-          // chunk max below 2^e; X = x 2^(22 - e), |X| <= 2^22
-          const int e = (int)((__float_as_uint(mx) >> 23) & 0xff) - 126;
-          const int sh = 22 - e;
-          if ((lane & 7) == 0) s_xsum[tid >> 3] = t, s_xsum[64 + (tid >> 3)] = __builtin_ldexpf(1.f, -sh);
-          // V = (X + 0x888888) ^ 0x888888: nibble k of V is balanced digit k of X as an int4
-          const float xv4[4] = {xn.x, xn.y, xn.z, xn.w};
-          uint32_t V[4];
-#pragma unroll
-          for (int t4 = 0; t4 < 4; ++t4) V[t4] = ((uint32_t)__float2int_rn(__builtin_ldexpf(xv4[t4], sh)) + 0x888888u) ^ 0x888888u;
-          // digit word (chunk c, 8-group gi, digit k) at 32-bit word ((gi 6 + k) / 4 * 64 + c) * 4 + (gi 6 + k) % 4;
-          // this thread holds inputs 4 h .. 4 h + 3 of the group: half h of the word
-          uint16_t* xd = reinterpret_cast<uint16_t*>(xq4);
-          const int c = tid >> 3, gi = (tid & 7) >> 1, h = tid & 1;
-#pragma unroll
-          for (int k = 0; k < 6; ++k) {
-            const uint32_t hw = ((V[0] >> (4 * k)) & 15u) | (((V[1] >> (4 * k)) & 15u) << 4) |
-                                (((V[2] >> (4 * k)) & 15u) << 8) | (((V[3] >> (4 * k)) & 15u) << 12);
-            const int j = gi * 6 + k;
-            xd[(((j >> 2) * 64 + c) * 4 + (j & 3)) * 2 + h] = (uint16_t)hw;
-          }
-        }
+        if constexpr (F::kMinTerm)  // threads 8c .. 8c + 7 hold chunk c
+          q4_digits_stage(xn, tid >> 3, tid & 7, reinterpret_cast<uint32_t*>(xq4), s_xsum, s_xsum + 64);
       };
       if (!is_router) stage_xq();
       if (is_router) {

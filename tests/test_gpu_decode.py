@@ -213,3 +213,33 @@ def test_decode_prefetch_range_is_harmless():
         torch.cuda.synchronize()
         outs.append(host(out))
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("case", ["zero_chunks", "wide_range", "wide_range_no_norm"])
+def test_decode_fixed_point_x_edge_cases(case):
+    """The int4 gate_up dots take x per 32-input chunk as 24-bit fixed point scaled to the
+    chunk's largest |x|: all-zero chunks and chunks mixing values 2^30 apart (after the norm,
+    and as raw x without it) must stay within the tolerance of the oracle's fp64 dots."""
+    E = 64
+    Lh = layer(11, E, "cfg")
+    dl = DevLayer(Lh)
+    rng = np.random.default_rng(21)
+    x = rng.normal(0, 1, 2048).astype(np.float32)
+    if case == "zero_chunks":
+        x[0:32] = 0.0
+        x[32 * 7:32 * 9] = 0.0
+        x[-32:] = 0.0
+    elif case == "wide_range":
+        x[::32] *= np.float32(2.0 ** 15)
+        x[1::32] *= np.float32(2.0 ** -15)
+    else:
+        x[::32] *= np.float32(2.0 ** 4)
+        x[1::32] *= np.float32(2.0 ** -26)
+    res = rng.normal(0, 1, 2048).astype(np.float32)
+    nw_on = case != "wide_range_no_norm"
+    nw = Lh["nw"] if nw_on else None
+    _, idx, wts, sg = O.router_topk(Lh["router"], x, nw, 1e-6, E, 8)
+    ract, ry = O.moe_decode(Lh, x, idx, wts, sg, res, 2048, 512, 8, nw=nw, eps=1e-6)
+    act, y = run_decode(dl, "cfg", x, idx, wts, sg, res, nw=nw_on)
+    assert_close(act, ract, what=f"act ({case})")
+    assert_close(y, ry, what=f"y ({case})")

@@ -249,8 +249,10 @@ struct StepQ4 {
   // -> 9.93-9.95; kOffActIb 310 -> 10.43, 320 -> 10.14, 330-340 -> 9.94-9.96, 360 -> 10.20)
   // (retuned for the integer-digit gate_up dots, whose pairs are done ~0.4 us sooner: kOffActIb 330 ->
   // 10.11, 310 -> 9.88, 290-300 -> 9.85 with kOffX 165, 9.68-9.70 with kOffX 180 (170 -> 9.75, 195 -> 9.84,
-  // 210 -> 9.96); kOffL 125 -> 9.64, 130 -> 9.57, 135 -> 9.59, 140 -> 9.64, 155 -> 9.78 us/layer)
-  static constexpr uint32_t kOffL = 130, kOffAct = 300, kOffX = 180;
+  // 210 -> 9.96); kOffL 125 -> 9.64, 130 -> 9.57, 135 -> 9.59, 140 -> 9.64, 155 -> 9.78 us/layer;
+  // on a second box with kOffActIb 295: kOffX 180 -> 9.50-9.54, 172 -> 9.44-9.50, 165 -> 9.41-9.46,
+  // 160 -> 9.41-9.43, the first box flat over 170-185: 165 sits inside both plateaus)
+  static constexpr uint32_t kOffL = 130, kOffAct = 300, kOffX = 165;
   static constexpr uint32_t kOffXA32 = 235;  // residual offset with the full-fp32 activation exchange
                                              // (190 -> 11.95, 215 -> 11.6-11.7, 235 -> 11.5 us/layer)
   // with the in-band activation phase (measured: 330 -> 12.7, 355 -> 11.8, 370-380 -> 11.4,

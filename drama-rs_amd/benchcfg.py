@@ -141,7 +141,8 @@ class Prefill:
                               self.sp)
         self.grouped = True
 
-    def experts(self, lib, L, fp8=False, shared_started=False):
+    def experts(self, lib, L, fp8=False, shared_started=False, packed=False):
+        """packed: L's routed experts are in the tile-step layout (packed_q4)."""
         P, sp = D.ptr, self.sp
         if not shared_started:
             self.shared_begin(lib, L)
@@ -149,7 +150,8 @@ class Prefill:
             lib.dr_moe_group_rows(P(self.idx), self.rows, TOPK, E, P(self.counts), P(self.offsets), P(self.slot_of),
                                   P(self.row_of_slot), sp)
         self.grouped = False
-        f = lib.dr_moe_prefill_rows_fp8_bf16s if fp8 else lib.dr_moe_prefill_rows_bf16s
+        f = (lib.dr_moe_prefill_rows_fp8_bf16s if fp8 else
+             lib.dr_moe_prefill_rows_packed_bf16s if packed else lib.dr_moe_prefill_rows_bf16s)
         f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.hn), self.rows, P(self.row_of_slot),
           P(self.offsets), P(self.counts), P(self.act), P(self.yp), E, H, I, sp)
         if self.overlap:
@@ -170,32 +172,51 @@ class Prefill:
         return hit * per_expert + shared + (L["router"].numel() * 2 if include_router else 0) + acts, hit
 
 
+def packed_q4(lib, L, st):
+    """L with its routed experts in the tile-step layout of dr_moe_pack_q4 (a second copy, made
+    once and kept in L)."""
+    if "pk" not in L:
+        P = D.ptr
+        pk = dict(L)
+        for q, sc, n, k in (("gu_q", "gu_s", 2 * I, H), ("d_q", "d_s", H, I)):
+            pk[q], pk[sc] = torch.empty_like(L[q]), torch.empty_like(L[sc])
+            lib.dr_moe_pack_q4(P(L[q]), P(L[sc]), E, n, k, P(pk[q]), P(pk[sc]), st.cuda_stream)
+        st.synchronize()
+        L["pk"] = pk
+    return L["pk"]
+
+
 def config4_prefill(lib, layers, st, iters=40, overlap=True):
-    """300 token rows, top-8 of 256 (2400 pairs), rotated over the 40 resident layers."""
+    """300 token rows, top-8 of 256 (2400 pairs), rotated over the 40 resident layers; the
+    routed experts read from their tile-step copy (packed_q4), the reference layout beside it."""
     pf = Prefill(300, st, overlap)
     nl = len(layers)
+    pl = [packed_q4(lib, L, st) for L in layers]
 
-    def full(i):
-        L = layers[i % nl]
+    def full(i, packed=True):
+        L = (pl if packed else layers)[i % nl]
         pf.shared_begin(lib, L)
         pf.router(lib, L)
-        pf.experts(lib, L, shared_started=True)
+        pf.experts(lib, L, shared_started=True, packed=packed)
 
+    ms_ref = timed(lambda i: full(i, False), iters, st)
     ms = timed(full, iters, st)
     msg = timed_graph(full, iters, st, min(nl, 8))
     nbytes, hit = pf.layer_bytes(layers[0])
     cnt = pf.counts.cpu()
     uniform = rec(ms * 1000, nbytes, experts_hit=hit, rows_per_expert_max=int(cnt.max()), pairs=pf.n,
-                  us_graph=round(msg * 1000, 2),
-                  note="router GEMM + top-k with grouping + grouped GEMM (token rows read through the slot map) + combine" + (
+                  us_graph=round(msg * 1000, 2), us_reference_layout=round(ms_ref * 1000, 2),
+                  note="router GEMM + top-k with grouping + grouped GEMM (token rows read through the slot map, "
+                       "experts in the tile-step layout) + combine" + (
                       ", the shared expert on a second stream beside them" if pf.overlap else " + shared, one stream")
-                       + "; us_graph: replayed from a HIP graph")
+                       + "; us_graph: replayed from a HIP graph; us_reference_layout: the experts read in the "
+                         "reference layout (dr_moe_prefill_rows_bf16s)")
     # the same 300 rows' experts (routing of the last uniform call) two ways: the grouped MFMA
     # path (grouping, gate_up, down, combine, shared expert) and the small-batch GEMV kernels
     # (dr_moe_decode_rows_bf16s: each weight row read once per 60-row call and multiplied by
     # every row routed to it with VALU FMAs), 5 calls of 60 rows
     pf.grouped = False
-    ms_mfma = timed(lambda i: pf.experts(lib, layers[i % nl]), iters, st)
+    ms_mfma = timed(lambda i: pf.experts(lib, pl[i % nl], packed=True), iters, st)
     P = D.ptr
     rows_c = 60
     xg = pf.x.clone()
@@ -213,7 +234,7 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
     ms_gemv = timed(gemv_path, max(4, iters // 4), st)
     mfma_vs_gemv = {"mfma_grouped_us": round(ms_mfma * 1000, 2), "gemv_rows_us": round(ms_gemv * 1000, 2),
                     "rows_per_expert_mean": round(pf.n / max(1, hit), 2),
-                    "note": "experts of one 300-row layer (routing given): grouped MFMA kernels (grouping, gate_up, "
+                    "note": "experts of one 300-row layer (routing given): grouped MFMA kernels on the tile-step copy (grouping, gate_up, "
                             "down, combine, shared expert) against the small-batch GEMV kernels "
                             "(dr_moe_decode_rows_bf16s, 5 calls of 60 rows, shared expert and residual included)"}
     # skewed routing: 10% of experts receive 50% of the pairs (synthetic indices)
@@ -226,7 +247,7 @@ def config4_prefill(lib, layers, st, iters=40, overlap=True):
     pf.wts.fill_(1.0 / TOPK)
 
     def skewed(i):
-        pf.experts(lib, layers[i % nl])
+        pf.experts(lib, pl[i % nl], packed=True)
 
     ms2 = timed(skewed, iters, st)
     nbytes2, hit2 = pf.layer_bytes(layers[0], include_router=False)

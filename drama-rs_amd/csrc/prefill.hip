@@ -284,7 +284,10 @@ DEV uint4 q4_frag(uint32_t w, uint32_t m, uint32_t b) {
 // B = weights (lane: row l % 16), so D[token 4 (l / 16) + i][row l % 16] sits in lane l: one
 // weight row per lane, one (scale, min) pair per group.  The group input sums X_g come from an
 // MFMA against bf16 ones (int4: staged with the tokens).
-template <class F, int MODE, int K, bool GATHER>
+// PK (int4 only): the weights are in the tile-step layout of dr_moe_pack_q4, so each step of a
+// wave is one contiguous 2048-byte block (two 1024-byte wave loads) and 256 bytes of scales,
+// where the reference layout gives 16 rows x 128 bytes 1 KB apart.
+template <class F, int MODE, int K, bool GATHER, bool PK = false>
 __global__ void __launch_bounds__(PF_GWPB * 64)
     k_grouped(const uint8_t* __restrict__ Wq, const void* __restrict__ Ws, const uint16_t* __restrict__ X,
               const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int N,
@@ -396,7 +399,17 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   };
   auto fetch = [&](const Item& it, int s, Step<F>& st) {
     const size_t n = row_of(it, s / SPT);
-    load_step<F>(it.wq + n * rb, it.ws, n, (s % SPT) * 4, g, K, st);
+    if constexpr (PK) {
+      static_assert(F::paired, "the tile-step layout is the int4 one");
+      // block (tile n / 16, step): lane l's 16 bytes of each half are what load_step reads
+      const size_t blk = (n >> 4) * SPT + (size_t)(s % SPT);
+      const uint8_t* tb = it.wq + blk * 2048;
+      st.raw[0] = ld16(tb + lane * 16);
+      st.raw[1] = ld16(tb + 1024 + lane * 16);
+      st.sc = ld16(reinterpret_cast<const uint8_t*>(it.ws) + blk * 256 + c16 * 16);
+    } else {
+      load_step<F>(it.wq + n * rb, it.ws, n, (s % SPT) * 4, g, K, st);
+    }
   };
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
   // the int4 conversion constants live in VGPRs: v_and_or_b32 (VOP3) takes no literal
@@ -891,7 +904,7 @@ inline int resident_blocks(const void* kern, int threads, size_t lds) {
 template <class F>
 void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const int* offsets, const int* counts,
                     void* out, int E, int N, int K, int mode, size_t eq, size_t es, int sb, int fixed_rows,
-                    hipStream_t st, const int* rmap = nullptr, int x_rows = 0) {
+                    hipStream_t st, const int* rmap = nullptr, int x_rows = 0, bool packed = false) {
   const int rows_out = mode == 0 ? N / 2 : N;
   if (fixed_rows >= 0) {
     // one weight set over all rows (the shared expert).  gate_up: the K-split kernel, one
@@ -914,6 +927,11 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
   const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
                      (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0);
   auto kern = mode == 1 ? k_grouped<F, 1, 512, false> : rmap ? k_grouped<F, 0, 2048, true> : k_grouped<F, 0, 2048, false>;
+  if constexpr (F::paired) {
+    if (packed)
+      kern = mode == 1 ? k_grouped<F, 1, 512, false, true>
+                       : rmap ? k_grouped<F, 0, 2048, true, true> : k_grouped<F, 0, 2048, false, true>;
+  }
   int grid = resident_blocks((const void*)kern, PF_GWPB * 64, lds);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(PF_GWPB * 64), lds, st, wq, ws, X, offsets, counts, out, N, eq, es, sb, E,
                      err_word(), rmap, x_rows);
@@ -925,11 +943,12 @@ template <class F>
 int moe_prefill(const uint8_t* gu_q, const void* gu_s, const uint8_t* d_q, const void* d_s, const uint16_t* xp,
                 const int* offsets, const int* counts, uint16_t* act, float* y, int E, int H, int I, size_t gu_q_b,
                 size_t gu_s_e, size_t d_q_b, size_t d_s_e, int sb, hipStream_t st, const int* rmap = nullptr,
-                int x_rows = 0) {
+                int x_rows = 0, bool packed = false) {
   if (H != 2048 || I != 512 || E < 1 || E > PF_MAXE) return -1;
   if (rmap && (x_rows < 1 || (long long)x_rows * H * 2 > 0x7fffffffll)) return -1;
-  launch_grouped<F>(gu_q, gu_s, xp, offsets, counts, act, E, 2 * I, H, 0, gu_q_b, gu_s_e, sb, -1, st, rmap, x_rows);
-  launch_grouped<F>(d_q, d_s, act, offsets, counts, y, E, H, I, 1, d_q_b, d_s_e, sb, -1, st);
+  launch_grouped<F>(gu_q, gu_s, xp, offsets, counts, act, E, 2 * I, H, 0, gu_q_b, gu_s_e, sb, -1, st, rmap, x_rows,
+                    packed);
+  launch_grouped<F>(d_q, d_s, act, offsets, counts, y, E, H, I, 1, d_q_b, d_s_e, sb, -1, st, nullptr, 0, packed);
   return 0;
 }
 
@@ -942,6 +961,34 @@ int shared_prefill(const int8_t* sgu_q, const uint16_t* sgu_s, const int8_t* sd_
   launch_grouped<FmtQ8<SH>>((const uint8_t*)sgu_q, sgu_s, hn, nullptr, nullptr, act, 1, 2 * I, H, 0, 0, 0, 2, rows, st);
   launch_grouped<FmtQ8<SH>>((const uint8_t*)sd_q, sd_s, act, nullptr, nullptr, out, 1, H, I, 1, 0, 0, 2, rows, st);
   return 0;
+}
+
+// int4 experts [e][n][k / 2] with (scale, min) words [e][n][k / 64] -> the tile-step layout of
+// k_grouped<..., PK>: for tile t (rows 16 t .. 16 t + 15) and step st (inputs 256 st ..
+// 256 st + 255), block t * (k / 256) + st holds 2048 bytes, byte p 1024 + 16 l + b = byte
+// 128 st + 64 p + 16 (l >> 4) + b of row 16 t + (l & 15), and 256 bytes of scales, word
+// 4 r + w = scale word 4 st + w of row 16 t + r.  One thread per 16 bytes of either.
+__global__ void __launch_bounds__(256)
+    k_pack_q4(const uint8_t* __restrict__ q, const uint32_t* __restrict__ sm, uint8_t* __restrict__ qo,
+              uint32_t* __restrict__ so, int n, int k, size_t nq, size_t ns) {
+  const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const int spt = k / 256;
+  if (c < nq) {
+    const size_t per_e = (size_t)n * (k / 2) / 16;
+    const size_t e = c / per_e, r = c % per_e, blk = r / 128;
+    const int p = (int)((r % 128) / 64), l = (int)(r % 64);
+    const size_t t = blk / spt, stp = blk % spt;
+    const size_t row = 16 * t + (l & 15);
+    const size_t src = e * per_e * 16 + row * (k / 2) + stp * 128 + p * 64 + (l >> 4) * 16;
+    *reinterpret_cast<uint4*>(qo + c * 16) = *reinterpret_cast<const uint4*>(q + src);
+  } else if (c < nq + ns) {
+    const size_t cs = c - nq;
+    const size_t per_e = (size_t)n * (k / 64) / 4;
+    const size_t e = cs / per_e, r = cs % per_e, blk = r / 16;
+    const size_t t = blk / spt, stp = blk % spt, row = 16 * t + r % 16;
+    const size_t src = e * per_e * 4 + row * (k / 64) + stp * 4;
+    *reinterpret_cast<uint4*>(so + cs * 4) = *reinterpret_cast<const uint4*>(sm + src);
+  }
 }
 
 }  // namespace
@@ -1022,4 +1069,34 @@ API int dr_moe_shared_prefill_bf16s(const int8_t* sgu_q, const uint16_t* sgu_s, 
                                     const uint16_t* hn, int rows, uint16_t* act, float* out, int H, int I,
                                     hipStream_t st) {
   return shared_prefill<Q8RowBF16>(sgu_q, sgu_s, sd_q, sd_s, hn, rows, act, out, H, I, st);
+}
+
+API int dr_moe_pack_q4(const uint8_t* q, const uint16_t* sm, int e, int n, int k, uint8_t* q_out, uint16_t* sm_out,
+                       hipStream_t st) {
+  if (e < 1 || n < 16 || n % 16 || k < 256 || k % 256 || !q || !sm || !q_out || !sm_out) return -1;
+  const size_t nq = (size_t)e * n * (k / 2) / 16, ns = (size_t)e * n * (k / 64) / 4;
+  const size_t blocks = (nq + ns + 255) / 256;
+  hipLaunchKernelGGL(k_pack_q4, dim3((unsigned)blocks), dim3(256), 0, st, q, reinterpret_cast<const uint32_t*>(sm),
+                     q_out, reinterpret_cast<uint32_t*>(sm_out), n, k, nq, ns);
+  return 0;
+}
+
+API int dr_moe_prefill_rows_packed(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q,
+                                   const uint16_t* d_sm, const uint16_t* x, int x_rows, const int* row_of_slot,
+                                   const int* offsets, const int* counts, uint16_t* act, float* y, int E, int H, int I,
+                                   hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtQ4<ScaleF16>>(gu_q, gu_sm, d_q, d_sm, x, offsets, counts, act, y, E, H, I,
+                                      (size_t)2 * I * (H / 2), (size_t)2 * I * (H / 64) * 2, (size_t)H * (I / 2),
+                                      (size_t)H * (I / 64) * 2, 2, st, row_of_slot, x_rows, true);
+}
+
+API int dr_moe_prefill_rows_packed_bf16s(const uint8_t* gu_q, const uint16_t* gu_sm, const uint8_t* d_q,
+                                         const uint16_t* d_sm, const uint16_t* x, int x_rows, const int* row_of_slot,
+                                         const int* offsets, const int* counts, uint16_t* act, float* y, int E, int H,
+                                         int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtQ4<ScaleBF16>>(gu_q, gu_sm, d_q, d_sm, x, offsets, counts, act, y, E, H, I,
+                                       (size_t)2 * I * (H / 2), (size_t)2 * I * (H / 64) * 2, (size_t)H * (I / 2),
+                                       (size_t)H * (I / 64) * 2, 2, st, row_of_slot, x_rows, true);
 }

@@ -70,6 +70,12 @@ def test_checkpoint_prefill_chunked(tmp_path):
         st.prefill(0, xc.view(rows, H), dhn.view(rows, H), chunk=128)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bits(host(xa)), bits(host(xc)))
+    # the tile-step copy of the experts (pack_prefill): the same bits
+    sp = C.MoeStack(str(tmp_path), pack_prefill=True)
+    xd = dev(x0)
+    sp.prefill(0, xd.view(rows, H), dhn.view(rows, H), chunk=128)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(host(xa)), bits(host(xd)))
     L = layers[0]
     rl = O.router_logits_rows(hn, L["router"], rows, E + 1, H)
     ri, rw, rs = O.moe_topk(rl, rows, E, 8, E + 1)

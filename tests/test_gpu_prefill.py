@@ -495,3 +495,66 @@ def test_group_rows_matches_oracle(rows, E, skew):
         np.testing.assert_array_equal(host(offsets), ro)
         np.testing.assert_array_equal(host(slot_of), rso)
         np.testing.assert_array_equal(host(row_of_slot)[rso], np.arange(n) // topk)
+
+
+def _pack_ref(q, sm, n, k):
+    """Host restatement of the tile-step layout of dr_moe_pack_q4 (include/drama_moe.h)."""
+    e = q.shape[0]
+    spt = k // 256
+    qv = q.reshape(e, n // 16, 16, spt, 2, 4, 16)      # [e][tile][row][step][p][g][b]
+    qo = qv.transpose(0, 1, 3, 4, 5, 2, 6)              # [e][tile][step][p][g][row][b]: lane l = 16 g + row
+    sv = sm.reshape(e, n // 16, 16, spt, 4, 2)          # [e][tile][row][step][word][half]
+    so = sv.transpose(0, 1, 3, 2, 4, 5)                 # [e][tile][step][row][word][half]
+    return np.ascontiguousarray(qo).reshape(e, n * k // 2), np.ascontiguousarray(so).reshape(e, n * k // 32)
+
+
+@pytest.mark.parametrize("e,n,k", [(3, 1024, 2048), (2, 2048, 512), (1, 16, 256)])
+def test_pack_q4_layout(e, n, k):
+    """dr_moe_pack_q4 against a numpy restatement of the layout, byte for byte."""
+    import torch
+
+    rng = np.random.default_rng(n + k + e)
+    q = rng.integers(0, 256, (e, n, k // 2), dtype=np.uint8)
+    sm = rng.integers(0, 65536, (e, n, k // 64, 2), dtype=np.uint16)
+    dq, ds = dev(q), dev(sm)
+    qo = torch.zeros(q.size, dtype=torch.uint8, device="cuda")
+    so = torch.zeros(sm.size, dtype=torch.int16, device="cuda")
+    D.lib().dr_moe_pack_q4(D.ptr(dq), D.ptr(ds), e, n, k, D.ptr(qo), D.ptr(so), D.stream_ptr())
+    torch.cuda.synchronize()
+    rq, rs = _pack_ref(q, sm, n, k)
+    np.testing.assert_array_equal(host(qo).reshape(e, -1), rq)
+    np.testing.assert_array_equal(host(so).view(np.uint16).reshape(e, -1), rs)
+    assert D.lib().raw("dr_moe_pack_q4")(D.ptr(dq), D.ptr(ds), e, 24, k, D.ptr(qo), D.ptr(so), None) == -1
+
+
+@pytest.mark.parametrize("fmt,skew,E,rows", [("cfg", False, 24, 96), ("ref", False, 24, 96), ("cfg", True, 24, 96),
+                                             ("cfg", False, 256, 300), ("cfg", True, 256, 300), ("cfg", False, 256, 1)])
+def test_prefill_rows_packed_matches(fmt, skew, E, rows):
+    """dr_moe_prefill_rows_packed*: weights packed by dr_moe_pack_q4 give the act and y bits of
+    dr_moe_prefill_rows* on the reference layout."""
+    import torch
+
+    topk = 8
+    Lh = synth.make_layer(40, E=E, fmt=fmt, kind="q4")
+    idx, counts, offsets, slot_of, x, xp = grouped_inputs(45 + rows, E, rows, topk, skew)
+    n = rows * topk
+    ros = np.zeros(n + 16, np.int32)
+    ros[slot_of] = np.arange(n) // topk
+    t = {k: dev(Lh[k]) for k in ("gu_q", "gu_s", "d_q", "d_s")}
+    pk = {k: torch.zeros_like(v) for k, v in t.items()}
+    lib = D.lib()
+    lib.dr_moe_pack_q4(D.ptr(t["gu_q"]), D.ptr(t["gu_s"]), E, 2 * I, H, D.ptr(pk["gu_q"]), D.ptr(pk["gu_s"]),
+                       D.stream_ptr())
+    lib.dr_moe_pack_q4(D.ptr(t["d_q"]), D.ptr(t["d_s"]), E, H, I, D.ptr(pk["d_q"]), D.ptr(pk["d_s"]), D.stream_ptr())
+    dx, dros, doff, dcnt = dev(x), dev(ros), dev(offsets), dev(counts)
+    outs = []
+    for packed, w in ((False, t), (True, pk)):
+        act = torch.zeros(n * I, dtype=torch.int16, device="cuda")
+        yp = torch.zeros(n * H, dtype=torch.float32, device="cuda")
+        name = "dr_moe_prefill_rows" + ("_packed" if packed else "") + ("_bf16s" if fmt == "cfg" else "")
+        getattr(lib, name)(D.ptr(w["gu_q"]), D.ptr(w["gu_s"]), D.ptr(w["d_q"]), D.ptr(w["d_s"]), D.ptr(dx), rows,
+                           D.ptr(dros), D.ptr(doff), D.ptr(dcnt), D.ptr(act), D.ptr(yp), E, H, I, D.stream_ptr())
+        torch.cuda.synchronize()
+        outs.append((host(act), host(yp)))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1].view(np.uint32), outs[0][1].view(np.uint32))

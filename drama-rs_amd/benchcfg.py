@@ -150,8 +150,10 @@ class Prefill:
             lib.dr_moe_group_rows(P(self.idx), self.rows, TOPK, E, P(self.counts), P(self.offsets), P(self.slot_of),
                                   P(self.row_of_slot), sp)
         self.grouped = False
-        f = (lib.dr_moe_prefill_rows_fp8_bf16s if fp8 else
-             lib.dr_moe_prefill_rows_packed_bf16s if packed else lib.dr_moe_prefill_rows_bf16s)
+        if fp8:
+            f = lib.dr_moe_prefill_rows_packed_fp8_bf16s if packed else lib.dr_moe_prefill_rows_fp8_bf16s
+        else:
+            f = lib.dr_moe_prefill_rows_packed_bf16s if packed else lib.dr_moe_prefill_rows_bf16s
         f(P(L["gu_q"]), P(L["gu_s"]), P(L["d_q"]), P(L["d_s"]), P(self.hn), self.rows, P(self.row_of_slot),
           P(self.offsets), P(self.counts), P(self.act), P(self.yp), E, H, I, sp)
         if self.overlap:
@@ -181,6 +183,19 @@ def packed_q4(lib, L, st):
         for q, sc, n, k in (("gu_q", "gu_s", 2 * I, H), ("d_q", "d_s", H, I)):
             pk[q], pk[sc] = torch.empty_like(L[q]), torch.empty_like(L[sc])
             lib.dr_moe_pack_q4(P(L[q]), P(L[sc]), E, n, k, P(pk[q]), P(pk[sc]), st.cuda_stream)
+        st.synchronize()
+        L["pk"] = pk
+    return L["pk"]
+
+
+def packed_fp8(lib, L, st):
+    """L with its routed e4m3 experts in the tile-step layout of dr_moe_pack_fp8 (scales shared)."""
+    if "pk" not in L:
+        pk = dict(L)
+        for q, n, k in (("gu_q", 2 * I, H), ("d_q", H, I)):
+            pk[q] = torch.empty_like(L[q])
+            if lib.dr_moe_pack_fp8(D.ptr(L[q]), E, n, k, D.ptr(pk[q]), st.cuda_stream) != 0:
+                raise RuntimeError("dr_moe_pack_fp8 rejected the layer")
         st.synchronize()
         L["pk"] = pk
     return L["pk"]
@@ -444,7 +459,24 @@ def config5_fp8(lib, st, iters=100, copies=4):
     out["decode_batch4_routed"] = rec(ms4f * 1000, nb4r, experts_hit=hit4, us_graph=round(ms4fg * 1000, 2),
                                       note="4 rows, router + top-k in the gate_up launch, then down "
                                            "(dr_moe_decode_rows_routed_fp8_bf16s, 2 launches); bytes as decode_batch4")
-    del L, Ls, routers
+    # 300-row prefill of the fp8 layer copies (configuration 4's shape), reference layout and
+    # tile-step copy (dr_moe_pack_fp8)
+    pf3 = Prefill(300, st)
+    pks = [packed_fp8(lib, Lc, st) for Lc in Ls]
+
+    def p300(i, packed):
+        Lc = (pks if packed else Ls)[i % copies]
+        pf3.router(lib, Lc)
+        pf3.experts(lib, Lc, fp8=True, packed=packed)
+
+    ms3 = timed(lambda i: p300(i, False), iters // 2, st)
+    ms3p = timed(lambda i: p300(i, True), iters // 2, st)
+    nb3, hit3 = pf3.layer_bytes(L)
+    out["prefill_fp8_300"] = rec(ms3p * 1000, nb3, experts_hit=hit3, us_reference_layout=round(ms3 * 1000, 2),
+                                 note="300 rows x top-8 of 256, fp8 experts read from their tile-step copy "
+                                      "(dr_moe_prefill_rows_packed_fp8_bf16s); us_reference_layout: "
+                                      "dr_moe_prefill_rows_fp8_bf16s on the [e][n][k] layout")
+    del L, Ls, routers, pks, pf3
     torch.cuda.empty_cache()
     # int8 lm_head 2048 x 151936 with per-row bf16 scales, and 2048 x 2048 projections
     g = torch.Generator(device="cuda").manual_seed(51)

@@ -183,9 +183,10 @@ class MoeStack:
     ``vram_layers`` (all when None) are uploaded to the GPU, the others stay in pinned host
     memory that the kernels read over PCIe (src/model.rs:81-97).
 
-    ``pack_prefill`` (int4 only) keeps a second copy of each layer's routed experts in the
-    tile-step layout of dr_moe_pack_q4, which prefill reads (the same results, less time; the
-    copy is as large as the experts, 6% of an MI355X's HBM for 40 layers)."""
+    ``pack_prefill`` keeps a second copy of each layer's routed experts in the tile-step layout
+    of dr_moe_pack_q4 (dr_moe_pack_fp8 for fp8 experts, whose scales are shared), which prefill
+    reads (the same results, less time; the int4 copy is as large as the experts, 6% of an
+    MI355X's HBM for 40 layers).  fp8 layers left in host memory are not packed."""
 
     def __init__(self, path: str, layers: list[int] | None = None, device: str = "cuda", fp8_dir: str | None = None,
                  vram_layers: int | None = None, pack_prefill: bool = False):
@@ -214,14 +215,23 @@ class MoeStack:
         self.sync = torch.zeros(4, dtype=torch.int32, device=device)
         self.lib = dramamoe.lib()
         self.packed = []  # per layer: the routed experts in the tile-step layout (pack_prefill)
-        if pack_prefill and not self.fp8:
+        if pack_prefill:
             P = dramamoe.ptr
             for L in self.layers:
-                pk = {}
+                if self.fp8 and not L["gu_q"].is_cuda:
+                    self.packed.append(None)
+                    continue
+                pk = dict(L) if self.fp8 else {}
                 for q, sc, n, k in (("gu_q", "gu_s", 2 * self.I, self.H), ("d_q", "d_s", self.H, self.I)):
-                    pk[q], pk[sc] = torch.empty_like(L[q]), torch.empty_like(L[sc])
-                    self.lib.dr_moe_pack_q4(P(L[q]), P(L[sc]), self.E, n, k, P(pk[q]), P(pk[sc]),
-                                            dramamoe.stream_ptr())
+                    pk[q] = torch.empty_like(L[q])
+                    if self.fp8:
+                        rc = self.lib.dr_moe_pack_fp8(P(L[q]), self.E, n, k, P(pk[q]), dramamoe.stream_ptr())
+                    else:
+                        pk[sc] = torch.empty_like(L[sc])
+                        rc = self.lib.dr_moe_pack_q4(P(L[q]), P(L[sc]), self.E, n, k, P(pk[q]), P(pk[sc]),
+                                                     dramamoe.stream_ptr())
+                    if rc != 0:
+                        raise ValueError(f"expert shape {n}x{k} has no tile-step layout")
                 self.packed.append(pk)
             torch.cuda.synchronize()
         self._gemm = {}  # stream handle -> GEMM handle (one per stream for the stack's lifetime)
@@ -315,9 +325,11 @@ class MoeStack:
             # through row_of_slot (no gathered copy)
             lib.dr_moe_topk_group(P(logits), n, E, k, E + 1, P(idx), P(wts), P(sg), P(counts), P(offsets),
                                   P(slot_of), P(row_of_slot), P(counter), st)
-            W = self.packed[l] if self.packed else L
-            pf = (lib.dr_moe_prefill_rows_fp8 if self.fp8 else
-                  lib.dr_moe_prefill_rows_packed if self.packed else lib.dr_moe_prefill_rows)
+            W = self.packed[l] if self.packed and self.packed[l] is not None else L
+            if self.fp8:
+                pf = lib.dr_moe_prefill_rows_packed_fp8 if W is not L else lib.dr_moe_prefill_rows_fp8
+            else:
+                pf = lib.dr_moe_prefill_rows_packed if W is not L else lib.dr_moe_prefill_rows
             pf(P(W["gu_q"]), P(W["gu_s"]), P(W["d_q"]), P(W["d_s"]), P(hr), n, P(row_of_slot), P(offsets), P(counts),
                P(act), P(yp), E, H, I, st)
             if overlap:

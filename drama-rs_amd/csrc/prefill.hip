@@ -54,6 +54,7 @@ struct FmtQ4 {
   static constexpr bool q8 = false;
   static constexpr bool has_min = true;
   static constexpr bool paired = true;  // k_grouped: 16-byte loads covering two groups per row
+  static constexpr bool packable = true;  // has a tile-step layout (dr_moe_pack_q4)
   static constexpr int scale_group = 64;  // inputs per scale
   static DEV size_t row_bytes(int K) { return (size_t)K / 2; }
   // fragment bytes of (row, group G) for lane group g: 8 bytes = 16 nibbles
@@ -79,6 +80,7 @@ struct FmtQ8 {
   static constexpr bool q8 = true;
   static constexpr bool has_min = false;
   static constexpr bool paired = false;
+  static constexpr bool packable = false;
   static constexpr int scale_group = SH::per_row ? 0 : 128;
   static DEV size_t row_bytes(int K) { return (size_t)K; }
   static DEV void load(const uint8_t* row, int G, int g, uint4& raw) { raw = ld16(row + G * 64 + g * 16); }
@@ -107,6 +109,7 @@ struct FmtFP8 {
   static constexpr bool q8 = false;
   static constexpr bool has_min = false;
   static constexpr bool paired = false;
+  static constexpr bool packable = true;  // has a tile-step layout (dr_moe_pack_fp8)
   static constexpr int scale_group = 128;
   static DEV size_t row_bytes(int K) { return (size_t)K; }
   static DEV void load(const uint8_t* row, int G, int g, uint4& raw) { raw = ld16(row + G * 64 + g * 16); }
@@ -399,14 +402,24 @@ __global__ void __launch_bounds__(PF_GWPB * 64)
   };
   auto fetch = [&](const Item& it, int s, Step<F>& st) {
     const size_t n = row_of(it, s / SPT);
-    if constexpr (PK) {
-      static_assert(F::paired, "the tile-step layout is the int4 one");
-      // block (tile n / 16, step): lane l's 16 bytes of each half are what load_step reads
+    if constexpr (PK && F::paired) {
+      // int4 block (tile n / 16, step): lane l's 16 bytes of each half are what load_step reads
       const size_t blk = (n >> 4) * SPT + (size_t)(s % SPT);
       const uint8_t* tb = it.wq + blk * 2048;
       st.raw[0] = ld16(tb + lane * 16);
       st.raw[1] = ld16(tb + 1024 + lane * 16);
       st.sc = ld16(reinterpret_cast<const uint8_t*>(it.ws) + blk * 256 + c16 * 16);
+    } else if constexpr (PK) {
+      // fp8 block (tile n / 16, step): 1024 bytes per group, lane l's 16 bytes of group i at
+      // i 1024 + 16 l (the block scales keep their layout)
+      static_assert(F::packable, "no tile-step layout for this format");
+      const size_t blk = (n >> 4) * SPT + (size_t)(s % SPT);
+      const uint8_t* tb = it.wq + blk * 4096;
+      const int G0 = (s % SPT) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.raw[i] = ld16(tb + i * 1024 + lane * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.sc[i] = F::scale_raw(it.ws, n, G0 + i, K);
     } else {
       load_step<F>(it.wq + n * rb, it.ws, n, (s % SPT) * 4, g, K, st);
     }
@@ -927,7 +940,7 @@ void launch_grouped(const uint8_t* wq, const void* ws, const uint16_t* X, const 
   const size_t lds = 2 * ((size_t)PF_TOK * K * 2 + (F::paired ? (size_t)(K / 64) * PF_TOK * 4 : 0)) + 192 * 16 +
                      (mode == 0 ? 2 * PF_GRPW * (PF_GWPB / 2) * 64 * 16 : 0);
   auto kern = mode == 1 ? k_grouped<F, 1, 512, false> : rmap ? k_grouped<F, 0, 2048, true> : k_grouped<F, 0, 2048, false>;
-  if constexpr (F::paired) {
+  if constexpr (F::packable) {
     if (packed)
       kern = mode == 1 ? k_grouped<F, 1, 512, false, true>
                        : rmap ? k_grouped<F, 0, 2048, true, true> : k_grouped<F, 0, 2048, false, true>;
@@ -989,6 +1002,23 @@ __global__ void __launch_bounds__(256)
     const size_t src = e * per_e * 4 + row * (k / 64) + stp * 4;
     *reinterpret_cast<uint4*>(so + cs * 4) = *reinterpret_cast<const uint4*>(sm + src);
   }
+}
+
+// e4m3 experts [e][n][k] -> the tile-step layout of k_grouped<FmtFP8, ..., PK>: block t * (k / 256)
+// + st of 4096 bytes (tile t of 16 rows, step st of 256 inputs), byte i 1024 + 16 l + b = byte
+// 256 st + 64 i + 16 (l >> 4) + b of row 16 t + (l & 15).  One thread per 16 bytes.
+__global__ void __launch_bounds__(256)
+    k_pack_fp8(const uint8_t* __restrict__ q, uint8_t* __restrict__ qo, int n, int k, size_t nq) {
+  const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= nq) return;
+  const int spt = k / 256;
+  const size_t per_e = (size_t)n * k / 16;
+  const size_t e = c / per_e, r = c % per_e, blk = r / 256;
+  const int i = (int)((r % 256) / 64), l = (int)(r % 64);
+  const size_t t = blk / spt, stp = blk % spt;
+  const size_t row = 16 * t + (l & 15);
+  const size_t src = e * per_e * 16 + row * k + stp * 256 + i * 64 + (l >> 4) * 16;
+  *reinterpret_cast<uint4*>(qo + c * 16) = *reinterpret_cast<const uint4*>(q + src);
 }
 
 }  // namespace
@@ -1099,4 +1129,31 @@ API int dr_moe_prefill_rows_packed_bf16s(const uint8_t* gu_q, const uint16_t* gu
   return moe_prefill<FmtQ4<ScaleBF16>>(gu_q, gu_sm, d_q, d_sm, x, offsets, counts, act, y, E, H, I,
                                        (size_t)2 * I * (H / 2), (size_t)2 * I * (H / 64) * 2, (size_t)H * (I / 2),
                                        (size_t)H * (I / 64) * 2, 2, st, row_of_slot, x_rows, true);
+}
+
+API int dr_moe_pack_fp8(const uint8_t* q, int e, int n, int k, uint8_t* q_out, hipStream_t st) {
+  if (e < 1 || n < 16 || n % 16 || k < 256 || k % 256 || !q || !q_out) return -1;
+  const size_t nq = (size_t)e * n * k / 16;
+  hipLaunchKernelGGL(k_pack_fp8, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, q, q_out, n, k, nq);
+  return 0;
+}
+
+API int dr_moe_prefill_rows_packed_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                                       const uint16_t* x, int x_rows, const int* row_of_slot, const int* offsets,
+                                       const int* counts, uint16_t* act, float* y, int E, int H, int I,
+                                       hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtFP8<0>>(gu_w, gu_s, d_w, d_s, x, offsets, counts, act, y, E, H, I, (size_t)2 * I * H,
+                                (size_t)(2 * I / 128) * (H / 128), (size_t)H * I, (size_t)(H / 128) * (I / 128), 4, st,
+                                row_of_slot, x_rows, true);
+}
+
+API int dr_moe_prefill_rows_packed_fp8_bf16s(const uint8_t* gu_w, const uint16_t* gu_s, const uint8_t* d_w,
+                                             const uint16_t* d_s, const uint16_t* x, int x_rows,
+                                             const int* row_of_slot, const int* offsets, const int* counts,
+                                             uint16_t* act, float* y, int E, int H, int I, hipStream_t st) {
+  if (!row_of_slot) return -1;
+  return moe_prefill<FmtFP8<1>>(gu_w, gu_s, d_w, d_s, x, offsets, counts, act, y, E, H, I, (size_t)2 * I * H,
+                                (size_t)(2 * I / 128) * (H / 128), (size_t)H * I, (size_t)(H / 128) * (I / 128), 2, st,
+                                row_of_slot, x_rows, true);
 }

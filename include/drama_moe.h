@@ -240,6 +240,21 @@ int dr_moe_prefill_rows_packed_bf16s(const uint8_t* gu_q, const dr_bf16* gu_sm, 
                                      const dr_bf16* d_sm, const dr_bf16* x, int x_rows, const int* row_of_slot,
                                      const int* offsets, const int* counts, dr_bf16* act, float* y, int e, int h,
                                      int i, dr_stream_t st);
+/* FP8 counterpart of dr_moe_pack_q4: e4m3 experts [e][n][k] -> q_out in the tile-step layout,
+ * block t (k / 256) + s of 4096 bytes (t: 16-row tile, s: 256-input step), byte
+ * 1024 p + 16 l + b = byte 256 s + 64 p + 16 (l >> 4) + b of row 16 t + (l & 15).  The 128x128
+ * block scales keep their layout and are passed unchanged.  Unsupported: n % 16, k % 256 -> -1.
+ * No reference counterpart. */
+int dr_moe_pack_fp8(const uint8_t* q, int e, int n, int k, uint8_t* q_out, dr_stream_t st);
+/* dr_moe_prefill_rows_fp8 / dr_moe_prefill_rows_fp8_bf16s with the expert weights packed by
+ * dr_moe_pack_fp8: the same act and y bits. */
+int dr_moe_prefill_rows_packed_fp8(const uint8_t* gu_w, const float* gu_s, const uint8_t* d_w, const float* d_s,
+                                   const dr_bf16* x, int x_rows, const int* row_of_slot, const int* offsets,
+                                   const int* counts, dr_bf16* act, float* y, int e, int h, int i, dr_stream_t st);
+int dr_moe_prefill_rows_packed_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, const uint8_t* d_w,
+                                         const dr_bf16* d_s, const dr_bf16* x, int x_rows, const int* row_of_slot,
+                                         const int* offsets, const int* counts, dr_bf16* act, float* y, int e,
+                                         int h, int i, dr_stream_t st);
 
 /* Prefill shared expert fused: act = bf16(silu(SG . hn) * (SU . hn)), out = SD . act (f32),
  * int8 weights dequantised in registers (replaces dr_dequant_q8 + dr_gemm + dr_swiglu_rows +

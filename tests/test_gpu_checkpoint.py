@@ -158,3 +158,13 @@ def test_checkpoint_fp8_source_step_chain_prefill(tmp_path):
     rl = O.router_logits_rows(hn, L["router"], rows, E + 1, H)
     ri, rw, rs = O.moe_topk(rl, rows, E, 8, E + 1)
     _check_prefill(L, hn, xp0, host(xa), kept, ri, rw, rs)
+    # pack_prefill: layer 0 (on the GPU) prefills from its tile-step copy, bit for bit the same;
+    # layer 1 (host memory) is left unpacked and runs on the reference layout
+    sp = C.MoeStack(str(conv), fp8_dir=str(src), vram_layers=1, pack_prefill=True)
+    assert sp.packed[0] is not None and sp.packed[1] is None
+    for l in (0, 1):
+        xr, xq = dev(xp0), dev(xp0)
+        st.prefill(l, xr.view(rows, H), dhn.view(rows, H))
+        sp.prefill(l, xq.view(rows, H), dhn.view(rows, H))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(host(xq)), bits(host(xr)), err_msg=f"layer {l}")

@@ -558,3 +558,58 @@ def test_prefill_rows_packed_matches(fmt, skew, E, rows):
         outs.append((host(act), host(yp)))
     np.testing.assert_array_equal(outs[1][0], outs[0][0])
     np.testing.assert_array_equal(outs[1][1].view(np.uint32), outs[0][1].view(np.uint32))
+
+
+def _pack_fp8_ref(q, n, k):
+    """Host restatement of the tile-step layout of dr_moe_pack_fp8 (include/drama_moe.h)."""
+    e = q.shape[0]
+    qv = q.reshape(e, n // 16, 16, k // 256, 4, 4, 16)   # [e][tile][row][step][p][g][b]
+    return np.ascontiguousarray(qv.transpose(0, 1, 3, 4, 5, 2, 6)).reshape(e, n * k)
+
+
+@pytest.mark.parametrize("e,n,k", [(2, 1024, 2048), (1, 16, 256)])
+def test_pack_fp8_layout(e, n, k):
+    """dr_moe_pack_fp8 against a numpy restatement of the layout, byte for byte."""
+    import torch
+
+    q = np.random.default_rng(n + k).integers(0, 256, (e, n, k), dtype=np.uint8)
+    dq = dev(q)
+    qo = torch.zeros(q.size, dtype=torch.uint8, device="cuda")
+    assert D.lib().raw("dr_moe_pack_fp8")(D.ptr(dq), e, n, k, D.ptr(qo), D.stream_ptr()) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(qo).reshape(e, -1), _pack_fp8_ref(q, n, k))
+    assert D.lib().raw("dr_moe_pack_fp8")(D.ptr(dq), e, n, 200, D.ptr(qo), None) == -1
+
+
+@pytest.mark.parametrize("fmt,skew,E,rows", [("cfg", False, 24, 96), ("ref", False, 24, 96), ("cfg", True, 256, 300),
+                                             ("cfg", False, 256, 1)])
+def test_prefill_rows_packed_fp8_matches(fmt, skew, E, rows):
+    """dr_moe_prefill_rows_packed_fp8*: weights packed by dr_moe_pack_fp8 give the act and y bits
+    of dr_moe_prefill_rows_fp8* on the reference layout."""
+    import torch
+
+    topk = 8
+    Lh = synth.make_layer(41, E=E, fmt=fmt, kind="fp8")
+    idx, counts, offsets, slot_of, x, xp = grouped_inputs(46 + rows, E, rows, topk, skew)
+    n = rows * topk
+    ros = np.zeros(n + 16, np.int32)
+    ros[slot_of] = np.arange(n) // topk
+    t = {k: dev(Lh[k]) for k in ("gu_q", "gu_s", "d_q", "d_s")}
+    pk = dict(t)
+    lib = D.lib()
+    for q, nn, kk in (("gu_q", 2 * I, H), ("d_q", H, I)):
+        pk[q] = torch.zeros_like(t[q])
+        assert lib.raw("dr_moe_pack_fp8")(D.ptr(t[q]), E, nn, kk, D.ptr(pk[q]), D.stream_ptr()) == 0
+    dx, dros, doff, dcnt = dev(x), dev(ros), dev(offsets), dev(counts)
+    outs = []
+    for packed, w in ((False, t), (True, pk)):
+        act = torch.zeros(n * I, dtype=torch.int16, device="cuda")
+        yp = torch.zeros(n * H, dtype=torch.float32, device="cuda")
+        name = "dr_moe_prefill_rows" + ("_packed" if packed else "") + "_fp8" + ("_bf16s" if fmt == "cfg" else "")
+        rc = lib.raw(name)(D.ptr(w["gu_q"]), D.ptr(w["gu_s"]), D.ptr(w["d_q"]), D.ptr(w["d_s"]), D.ptr(dx), rows,
+                           D.ptr(dros), D.ptr(doff), D.ptr(dcnt), D.ptr(act), D.ptr(yp), E, H, I, D.stream_ptr())
+        assert rc == 0, f"{name} returned {rc}"
+        torch.cuda.synchronize()
+        outs.append((host(act), host(yp)))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1].view(np.uint32), outs[0][1].view(np.uint32))

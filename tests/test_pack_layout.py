@@ -1,9 +1,10 @@
-"""The tile-step layout of dr_moe_pack_q4 (include/drama_moe.h): the numpy restatement the GPU
-test compares against (tests/test_gpu_prefill.py::_pack_ref, a reshape/transpose) checked
+"""The tile-step layouts of dr_moe_pack_q4 and dr_moe_pack_fp8 (include/drama_moe.h): the numpy
+restatements the GPU tests compare against (tests/test_gpu_prefill.py::_pack_ref and
+_pack_fp8_ref, reshape/transposes) checked
 element by element against the header's per-byte definition, on the CPU."""
 import numpy as np
 
-from test_gpu_prefill import _pack_ref
+from test_gpu_prefill import _pack_fp8_ref, _pack_ref
 
 
 def test_pack_ref_matches_the_byte_definition():
@@ -24,3 +25,18 @@ def test_pack_ref_matches_the_byte_definition():
                 for r in range(16):
                     for w in range(4):
                         np.testing.assert_array_equal(so[ee, (blk * 64 + 4 * r + w) * 2:][:2], sm[ee, 16 * t + r, 4 * s + w])
+
+
+def test_pack_fp8_ref_matches_the_byte_definition():
+    rng = np.random.default_rng(1)
+    for e, n, k in ((2, 32, 512), (1, 16, 256)):
+        spt = k // 256
+        q = rng.integers(0, 256, (e, n, k), dtype=np.uint8)
+        qo = _pack_fp8_ref(q, n, k)
+        for ee in range(e):
+            for blk in range(n // 16 * spt):
+                t, s = divmod(blk, spt)
+                for p in range(4):
+                    for lane in range(64):
+                        src = q[ee, 16 * t + (lane & 15), 256 * s + 64 * p + 16 * (lane >> 4):][:16]
+                        np.testing.assert_array_equal(qo[ee, blk * 4096 + p * 1024 + 16 * lane:][:16], src)

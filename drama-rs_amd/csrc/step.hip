@@ -477,7 +477,16 @@ __global__ void __launch_bounds__(ST_NT, 1)
   const int g = blockIdx.x * ST_WPB + wave;
   const uint32_t epoch = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tag0 = epoch * ST_TAG_STRIDE + 1;
-  const uint32_t lbase = __hip_atomic_load(sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t lbase_in = __hip_atomic_load(sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // sync[3]: the activation transport of the previous launch on this ll / sync pair (0 none, 1
+  // packed, 2 fp32 with tags).  After the other transport, words that launch left in the packed
+  // routed slots could pass for current ones (a tagged word's tag and value bits can carry the
+  // phase), so this launch clears those slots before its first exchange and restarts the phase
+  // count at a multiple of 4: the first layer's phase is then 1, which no cleared word carries.
+  constexpr uint32_t kTransport = A32 ? 2u : 1u;
+  const uint32_t prev_transport = __hip_atomic_load(sync + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool switched = prev_transport != 0 && prev_transport != kTransport;
+  const uint32_t lbase = switched ? (lbase_in + 3u) & ~3u : lbase_in;
 
   const bool is_router = (wave == 0 && (int)blockIdx.x <= E) || (wave == 1 && blockIdx.x == 0 && E == ST_MAXE);
   const int rrow = wave == 0 ? (int)blockIdx.x : ST_MAXE;
@@ -506,6 +515,13 @@ __global__ void __launch_bounds__(ST_NT, 1)
     if (L0.nw) nwv = ldf4(L0.nw + 4 * tid);
     nws[tid] = nwv;
     xr4[tid] = xv;
+  }
+  if (switched && tid < 2048 / ST_NB) {
+    // complete before the start-up barrier, so before this block's first logit is published:
+    // every block reads all logits before any activation is published or polled
+    __hip_atomic_store(ll + LL_ACT + blockIdx.x * (2048 / ST_NB) + tid, 0ull, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   }
   if (__syncthreads_or(gave_up != 0)) {
     give_up();
@@ -739,6 +755,7 @@ __global__ void __launch_bounds__(ST_NT, 1)
   }
   if (blockIdx.x == 0 && tid == 0) {
     __hip_atomic_store(sync + 2, lbase + (uint32_t)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync + 3, kTransport, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(sync, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // the caller's next-op range [pf, pf + pf_bytes) warmed in the memory-side cache, each block

@@ -387,7 +387,8 @@ typedef struct dr_decode_layer {
  * dr_moe_decode(x, res = x, y = x); routing is bit-exact with that chain.
  *   x         f32 [h], read at launch and overwritten with the last layer's output;
  *   ll        u64 [DR_STEP_LL_WORDS] exchange buffer, sync u32 [4]: both zeroed once by the
- *             caller before the first call and then left alone (a call advances sync[0]);
+ *             caller before the first call and then left alone (a call advances sync[0] and
+ *             sync[2], and records its activation transport in sync[3]);
  *             sync[1] != 0 reports that a call timed out waiting for its workgroups: that call
  *             leaves NaN in x (every block that gives up overwrites all of x with NaN; a block
  *             that completed its last layer may still store its own rows afterwards) and raises

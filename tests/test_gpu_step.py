@@ -118,6 +118,37 @@ def test_step_in_band_phase_over_launches_of_any_length():
         L.dr_step_set_act_exchange(0)
 
 
+def test_step_transport_switch_on_one_ll():
+    """Launches on one ll / sync pair that switch the activation transport (fp32 with tags ->
+    packed -> fp32 -> packed).  Before each packed launch the packed routed slots are filled with
+    junk (1e30) carrying the phase the launch would expect without the transport record in
+    sync[3]: the launch must clear them, so every launch still matches the oracle."""
+    import torch
+
+    st = Stack([720, 721], 64, "cfg")
+    L = D.lib()
+    x0 = np.random.default_rng(19).normal(0, 1, H).astype(np.float32)
+    xd = dev(x0)
+    act_words = slice(264, 264 + 2048)  # LL_ACT: the packed routed slots
+    try:
+        for call, bits_ in enumerate([32, 30, 32, 30, 30]):
+            print(f"transport switch launch {call}: {bits_} bit", flush=True)
+            L.dr_step_set_act_exchange(bits_)
+            if bits_ == 30 and call in (1, 3):
+                t2 = (int(host(st.sync)[2]) + 1) & 3
+                half = (np.float32(1e30).view(np.uint32) & ~np.uint32(3)) | np.uint32(t2)
+                junk = (np.uint64(half) << np.uint64(32)) | np.uint64(half)
+                st.ll[act_words] = torch.tensor(np.full(2048, junk, np.uint64).view(np.int64), device="cuda")
+                torch.cuda.synchronize()
+            xin = host(xd).copy()
+            idx, wts, sg, xs = st.run(xd)
+            assert int(host(st.sync)[1]) == 0, "step reported a timeout"
+            assert int(host(st.sync)[3]) == (2 if bits_ == 32 else 1), "transport record"
+            check_stack(st, xin, idx, wts, sg, xs, host(xd))
+    finally:
+        L.dr_step_set_act_exchange(0)
+
+
 @pytest.mark.parametrize("fmt,E,n,bits", [("cfg", 32, 3, 32), ("ref", 16, 2, 32), ("cfg", 8, 2, 32), ("cfg", 16, 1, 32),
                                           ("cfg", 32, 2, 30)])
 def test_step_fp8_matches_oracle_layer_by_layer(fmt, E, n, bits):

@@ -12,94 +12,6 @@ using namespace drm;
 
 namespace {
 
-// Decode router: wave w of block b computes logit row RT_WPB b + w of the E + 1 rows.  All
-// loads of a wave (its weight row, x for the norm, x and nw for its dot lanes) are issued
-// before any arithmetic.  Logits are published with cache-bypassing (sc1) stores; after its
-// stores have completed (s_waitcnt) each block counts itself in with one relaxed atomic, and
-// the last block reads the logits back with sc1 loads and runs softmax/top-k (group
-// selections on four waves and a rank merge for topk <= 8).  No cache-maintenance fence is needed: every cross-block value bypasses the
-// non-coherent caches.  The last block resets the counter for the next call.
-
-template <int K>
-__global__ void __launch_bounds__(RT_WPB * 64)
-    k_router_topk(const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ nw,
-                  float eps, float* __restrict__ logits, int E, int topk, int* __restrict__ idx,
-                  float* __restrict__ wts, float* __restrict__ sgate, uint32_t* __restrict__ counter) {
-  __shared__ int s_last;
-  const int lane = lane_id(), wave = wave_id();
-  const int row = blockIdx.x * RT_WPB + wave;
-  if (row <= E) {
-    constexpr int NCH = K / 8 / WAVE, NRM = K / 4 / WAVE;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const float4* n4 = reinterpret_cast<const float4*>(nw);
-    uint4 w[NCH];
-    float4 xa[NCH], xb[NCH], na[NCH], nb[NCH], xr[NRM];
-    const uint16_t* wr = W + (size_t)row * K;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) w[j] = ld16(wr + (size_t)(lane + WAVE * j) * 8);
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = lane + WAVE * j;
-      xa[j] = x4[2 * c], xb[j] = x4[2 * c + 1];
-    }
-    float inv = 1.f;
-    if (nw) {
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const int c = lane + WAVE * j;
-        na[j] = n4[2 * c], nb[j] = n4[2 * c + 1];
-      }
-#pragma unroll
-      for (int j = 0; j < NRM; ++j) xr[j] = x4[lane + WAVE * j];
-      inv = canon_rms_inv_regs<NRM>(xr, eps);
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) xa[j] = canon_norm4(xa[j], inv, na[j]), xb[j] = canon_norm4(xb[j], inv, nb[j]);
-    }
-    const float acc = canon_row_dot<NCH>(w, xa, xb);
-    if (lane == 0) __hip_atomic_store(logits + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // stage the logits (sc1 loads) in LDS, then the canonical softmax/top-k: for topk <= 8 the
-  // group selections on waves 0..3 and the denominator on wave 4 run side by side
-  __shared__ float lg[257];
-  __shared__ uint64_t s_cand[32];
-  __shared__ int s_sel[8];
-  __shared__ float s_mz[2];
-  if ((int)threadIdx.x <= E) lg[threadIdx.x] = __hip_atomic_load(logits + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (topk <= 8) {
-    if (wave < 4) {
-      int ck, ce;
-      canon_select_group8(lg, E, wave, &ck, &ce);
-      if (lane < 8) s_cand[wave * 8 + lane] = canon_cand64(ck, ce);
-    } else if (wave == 4) {
-      float m;
-      const float z = canon_softmax_z(lg, E, &m);
-      if (lane == 0) s_mz[0] = m, s_mz[1] = z;
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    const int id = merge_picks(s_cand, s_sel, topk);
-    const float w = canon_topk_weight(lg[lane < topk ? id : 0], s_mz[0], s_mz[1], topk);
-    if (lane < topk) idx[lane] = id, wts[lane] = w;
-  } else {
-    if (wave != 0) return;
-    int my_idx;
-    float my_w;
-    canon_softmax_topk(lg, E, topk, &my_idx, &my_w);
-    if (lane < topk) idx[lane] = my_idx, wts[lane] = my_w;
-  }
-  if (lane == 0) {
-    sgate[0] = lg[E];
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
 // Decode router for B rows (B <= 8) in one launch of router blocks (router_rows.hpp).
 template <int B>
 __global__ void __launch_bounds__(RT_WPB * 64)
@@ -334,8 +246,10 @@ API int dr_router_topk(const uint16_t* W, const float* x, const float* nw, float
                        int K, int* idx, float* wts, float* sgate, uint32_t* counter, const char*, const char*,
                        const char*, const char*, size_t, size_t, size_t, size_t, hipStream_t st) {
   if (K != 2048 || E > 256 || E < 1 || topk > 32 || topk < 1 || topk > E) return -1;
-  hipLaunchKernelGGL(k_router_topk<2048>, dim3((E + RT_WPB) / RT_WPB), dim3(RT_WPB * 64), 0, st, W, x, nw, eps, logits, E, topk,
-                     idx, wts, sgate, counter);
+  // the one-row case of the small-batch router (its one-wave top-k measured 0.3 us shorter per
+  // call than four group selections and a rank merge, with the same picks)
+  hipLaunchKernelGGL(k_router_topk_rows<1>, dim3((E + RT_WPB) / RT_WPB), dim3(RT_WPB * 64), 0, st, W, x, nw, eps, logits,
+                     E, topk, idx, wts, sgate, counter);
   return 0;
 }
 

@@ -1,14 +1,15 @@
-// Decode router for B rows (B <= 8) as one block's work: shared by dr_router_topk_rows (a
-// launch of router blocks only) and the fused small-batch FP8 kernel (router blocks ahead of
-// the gate_up blocks in one launch).  Reference semantics: kernels/drama.cu:317-461 per row.
+// Decode router for B rows (B <= 8) as one block's work: shared by dr_router_topk (B = 1),
+// dr_router_topk_rows (a launch of router blocks only) and the fused small-batch FP8 kernel
+// (router blocks ahead of the gate_up blocks in one launch).  Reference semantics:
+// kernels/drama.cu:317-461 per row.
 //
 // Block blk of nblk: wave w computes logit row RT_WPB blk + w for every row, its weight row
 // loaded once.  The rows of x are staged in LDS, wave r < B computes row r's canonical RMSNorm
 // scale, and the block normalises the staged rows in place (canon_norm4 is elementwise, so the
-// values equal those k_router_topk forms in registers).  Every logit has the canonical order
-// of canon.hpp, so each row's logits, picks and weights equal those of dr_router_topk on that
-// row.  Logits are published with cache-bypassing (sc1) stores; each block counts itself in
-// once its stores completed, and the last block loads the logits of all rows at once and
+// values equal those of the canonical norm in registers).  Every logit has the canonical order
+// of canon.hpp, so each row's logits, picks and weights equal the CPU oracle's on that row.
+// Logits are published with cache-bypassing (sc1) stores; each block counts itself in once its
+// stores completed, and the last block loads the logits of all rows at once and
 // spreads the per-row work over its waves: for topk <= 8 and 2 B <= RT_WPB one wave selects
 // each row's top-k over all its experts (canon_select_topk) beside the B softmax
 // denominators; above 4 rows the 4 B group selections come first and one rank merge per row

@@ -106,3 +106,19 @@ def test_oracle_is_not_linked_into_the_product():
     ldd = subprocess.run(["ldd", D.LIB_PATH], capture_output=True, text=True).stdout
     assert "liboracle" not in ldd
     assert not re.search(r" U or_", nm)
+
+
+def test_integration_bindings_match_header():
+    """The Rust extern block INTEGRATION.md gives a maintainer binds only declared entry points,
+    each with the header's argument count and kinds (pointers, i32, u32, usize, f32)."""
+    text = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
+    rust = _rust_decls(text)
+    ours = D.parse_header()
+    assert len(rust) >= 15
+    for name, kinds in rust.items():
+        assert name in ours, f"{name} (INTEGRATION.md) is not declared in include/drama_moe.h"
+        ck = ours[name][1]
+        assert len(ck) == len(kinds), f"{name}: header has {len(ck)} args, INTEGRATION.md {len(kinds)}"
+        for i, (a, b) in enumerate(zip(ck, kinds)):
+            a = "ptr" if a.startswith("dr_") and a.endswith("_t") else a
+            assert a == _C_OF_RUST.get(b, b), f"{name} arg {i}: {a} vs INTEGRATION.md {b}"

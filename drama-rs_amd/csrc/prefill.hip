@@ -1101,10 +1101,20 @@ API int dr_moe_shared_prefill_bf16s(const int8_t* sgu_q, const uint16_t* sgu_s, 
   return shared_prefill<Q8RowBF16>(sgu_q, sgu_s, sd_q, sd_s, hn, rows, act, out, H, I, st);
 }
 
+// [a, a + na) and [b, b + nb) share a byte
+static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
+
 API int dr_moe_pack_q4(const uint8_t* q, const uint16_t* sm, int e, int n, int k, uint8_t* q_out, uint16_t* sm_out,
                        hipStream_t st) {
   if (e < 1 || n < 16 || n % 16 || k < 256 || k % 256 || !q || !sm || !q_out || !sm_out) return -1;
   const size_t nq = (size_t)e * n * (k / 2) / 16, ns = (size_t)e * n * (k / 64) / 4;
+  const size_t qb = nq * 16, sb = ns * 16;  // bytes of the weights and of the scale words
+  if (overlaps(q_out, qb, q, qb) || overlaps(q_out, qb, sm, sb) || overlaps(sm_out, sb, q, qb) ||
+      overlaps(sm_out, sb, sm, sb) || overlaps(q_out, qb, sm_out, sb))
+    return -1;
   const size_t blocks = (nq + ns + 255) / 256;
   hipLaunchKernelGGL(k_pack_q4, dim3((unsigned)blocks), dim3(256), 0, st, q, reinterpret_cast<const uint32_t*>(sm),
                      q_out, reinterpret_cast<uint32_t*>(sm_out), n, k, nq, ns);
@@ -1134,6 +1144,7 @@ API int dr_moe_prefill_rows_packed_bf16s(const uint8_t* gu_q, const uint16_t* gu
 API int dr_moe_pack_fp8(const uint8_t* q, int e, int n, int k, uint8_t* q_out, hipStream_t st) {
   if (e < 1 || n < 16 || n % 16 || k < 256 || k % 256 || !q || !q_out) return -1;
   const size_t nq = (size_t)e * n * k / 16;
+  if (overlaps(q_out, nq * 16, q, nq * 16)) return -1;
   hipLaunchKernelGGL(k_pack_fp8, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, q, q_out, n, k, nq);
   return 0;
 }

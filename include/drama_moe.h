@@ -228,8 +228,8 @@ int dr_moe_prefill_rows_fp8_bf16s(const uint8_t* gu_w, const dr_bf16* gu_s, cons
  * sm_out by 256 bytes of its scale words (word 4 r + w = word 4 s + w of row 16 t + r).
  * Pack gu_q/gu_sm with n = 2i, k = h and d_q/d_sm with n = h, k = i.  The layout costs a second
  * copy of the routed experts (16.9 GiB for configuration 3's 40 layers, 6% of an MI355X's HBM)
- * and changes no result.  q_out / sm_out must not overlap q / sm (no in-place packing).
- * Unsupported: n % 16, k % 256 -> -1.  No reference counterpart. */
+ * and changes no result.  Unsupported: n % 16, k % 256, or outputs overlapping the inputs (no
+ * in-place packing) -> -1.  No reference counterpart. */
 int dr_moe_pack_q4(const uint8_t* q, const uint16_t* sm, int e, int n, int k, uint8_t* q_out, uint16_t* sm_out,
                    dr_stream_t st);
 /* dr_moe_prefill_rows / dr_moe_prefill_rows_bf16s with the expert weights packed by
@@ -244,8 +244,8 @@ int dr_moe_prefill_rows_packed_bf16s(const uint8_t* gu_q, const dr_bf16* gu_sm, 
 /* FP8 counterpart of dr_moe_pack_q4: e4m3 experts [e][n][k] -> q_out in the tile-step layout,
  * block t (k / 256) + s of 4096 bytes (t: 16-row tile, s: 256-input step), byte
  * 1024 p + 16 l + b = byte 256 s + 64 p + 16 (l >> 4) + b of row 16 t + (l & 15).  The 128x128
- * block scales keep their layout and are passed unchanged.  q_out must not overlap q.
- * Unsupported: n % 16, k % 256 -> -1.
+ * block scales keep their layout and are passed unchanged.  Unsupported: n % 16, k % 256, or
+ * q_out overlapping q -> -1.
  * No reference counterpart. */
 int dr_moe_pack_fp8(const uint8_t* q, int e, int n, int k, uint8_t* q_out, dr_stream_t st);
 /* dr_moe_prefill_rows_fp8 / dr_moe_prefill_rows_fp8_bf16s with the expert weights packed by

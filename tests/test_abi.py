@@ -122,3 +122,18 @@ def test_integration_bindings_match_header():
         for i, (a, b) in enumerate(zip(ck, kinds)):
             a = "ptr" if a.startswith("dr_") and a.endswith("_t") else a
             assert a == _C_OF_RUST.get(b, b), f"{name} arg {i}: {a} vs INTEGRATION.md {b}"
+
+
+def test_pack_entry_points_refuse_overlap_without_gpu():
+    """dr_moe_pack_q4 / dr_moe_pack_fp8 return -1 before any launch when an output overlaps an
+    input (host pointers: nothing is dereferenced on this path)."""
+    lib = D.lib()
+    buf = ctypes.create_string_buffer(1 << 20)
+    base = ctypes.addressof(buf)
+    q4 = lib.raw("dr_moe_pack_q4")
+    # e = 1, n = 16, k = 256: 2048 bytes of weights, 256 bytes of scale words
+    assert q4(base, base + 4096, 1, 16, 256, base + 1024, base + 8192, None) == -1  # q_out over q
+    assert q4(base, base + 4096, 1, 16, 256, base + 16384, base + 4096, None) == -1  # sm_out is sm
+    assert q4(base, base + 4096, 1, 16, 256, base + 16384, base + 17000, None) == -1  # q_out over sm_out
+    f8 = lib.raw("dr_moe_pack_fp8")
+    assert f8(base, 1, 16, 256, base + 2048, None) == -1  # 4096 bytes each, overlapping by half
